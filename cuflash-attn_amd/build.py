@@ -1,0 +1,86 @@
+"""Builds libcuflash_attn.so for gfx950 with hipcc.
+
+The shared library lands in <repo>/build/libcuflash_attn.so, one of the paths the reference's
+ctypes callers search (tests/integration/test_pytorch_comparison.py:158-180), with hidden default
+visibility so that only the CUFLASH_EXPORT symbols are exported (reference CMakeLists.txt:60-72).
+
+Usage: python cuflash-attn_amd/build.py [--jobs N]
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+BUILD_DIR = os.path.join(REPO_ROOT, "build")
+LIB_NAME = "libcuflash_attn.so"
+LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
+
+SOURCES = ["api.cpp", "forward.hip", "backward.hip", "decode.hip"]
+
+# Packed-FP32 VALU forms are disabled for all device code (v_pk_{add,mul,fma}_f32).
+COMMON_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-fvisibility-inlines-hidden",
+    "-DCUFLASH_BUILDING_SHARED",
+    "-I" + INCLUDE,
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found (ROCm is required to build libcuflash_attn)")
+    return path
+
+
+def _compile(src: str, obj: str) -> None:
+    cmd = [hipcc(), "-x", "hip", *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")
+
+
+def build(jobs: int = 4, verbose: bool = True) -> str:
+    """Compiles every source and links build/libcuflash_attn.so. Returns the library path."""
+    obj_dir = os.path.join(BUILD_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        futures = [pool.submit(_compile, s, o) for s, o in zip(SOURCES, objs)]
+        for f in futures:
+            f.result()
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=4)
+    args = ap.parse_args()
+    try:
+        build(args.jobs)
+    except RuntimeError as e:
+        print(e, file=sys.stderr)
+        sys.exit(1)

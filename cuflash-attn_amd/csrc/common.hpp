@@ -1,0 +1,248 @@
+#pragma once
+
+// Device-side building blocks shared by the gfx950 kernels: element traits for the three
+// storage types, CDNA4 MFMA wrappers, 16-byte vector I/O, wave reductions and the workgroup
+// scheduling helpers.
+//
+// MFMA register layouts used throughout (wave64, verified on gfx950):
+//   v_mfma_f32_32x32x16_{bf16,f16}:  A (32x16): lane l holds A[l%32][8*(l/32) + 0..7]
+//                                    B (16x32): lane l holds B[8*(l/32) + 0..7][l%32]
+//                                    C (32x32): lane l holds C[8*(r/4) + 4*(l/32) + r%4][l%32],
+//                                               r = 0..15
+//   v_mfma_f32_32x32x2f32:           A: lane l holds A[l%32][l/32]; B: B[l/32][l%32]; C as above.
+// Because the sum over k is order-free, a kernel may assign any logical k index to each
+// (lane-half, slot) pair as long as the A and B operands agree; the kernels use this to feed
+// an accumulator tile (C layout) straight back as the B operand of the next product.
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cuflash {
+namespace dev {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------------------------
+// Element traits. 16-bit types are moved around as raw uint16_t bit patterns; conversions use
+// the hardware round-to-nearest-even converts (v_cvt_pk_bf16_f32, v_cvt_f16_f32), matching the
+// reference's __float2bfloat16_rn / __float2half (src/kernels/impl/type_adapter.cuh:18-32).
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__hip_bfloat16> {
+    using frag = bf16x8;
+    static __device__ __forceinline__ float to_f(uint16_t v) {
+        return __uint_as_float(static_cast<uint32_t>(v) << 16);
+    }
+    // Two floats -> two RNE bf16 packed in one dword (low half = a).
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        bf16x2 r;
+        r[0] = static_cast<__bf16>(a);
+        r[1] = static_cast<__bf16>(b);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Elem<__half> {
+    using frag = f16x8;
+    static __device__ __forceinline__ float to_f(uint16_t v) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, v));
+    }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
+        const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
+        return lo | (hi << 16);
+    }
+    static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// 16 bytes of 16-bit elements reinterpreted as an MFMA operand.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag as_frag(u32x4 v) {
+    return __builtin_bit_cast(typename Elem<T>::frag, v);
+}
+
+// Eight floats -> eight 16-bit elements packed as an MFMA operand.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag pack_frag(float a0, float a1, float a2, float a3,
+                                                            float a4, float a5, float a6,
+                                                            float a7) {
+    u32x4 v;
+    v[0] = Elem<T>::pack2(a0, a1);
+    v[1] = Elem<T>::pack2(a2, a3);
+    v[2] = Elem<T>::pack2(a4, a5);
+    v[3] = Elem<T>::pack2(a6, a7);
+    return as_frag<T>(v);
+}
+
+__device__ __forceinline__ f32x16 mma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Global / LDS vector access
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+    return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Low / high 16-bit halves of two dwords packed into one dword.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ---------------------------------------------------------------------------------------------
+// LDS transpose read (gfx950 ds_read_b64_tr_b16).
+// Within each 16-lane group, result lane i, slot j (j = 0..3) is element i%4 of the 8-byte chunk
+// addressed by lane 4*j + i/4 of the same group (verified on gfx950). `read_tr_frag` uses it to
+// build a 32x32x16 operand whose k index runs down the ROWS of a row-major LDS matrix M
+// (pitch in elements): lane l receives M[k0 + kslot(l/32, t)][n0 + l%32] for t = 0..7, where
+// kslot(h, t) = 8*(t/4) + 4*h + t%4. This is the k assignment of an accumulator tile reused as
+// an operand (C-layout rows of one lane: 8*(r/4) + 4*(l/32) + r%4), so products such as P*V,
+// dS*K, P^T*dO and dS^T*Q read V, K, dO and Q in their natural row-major layout.
+// ---------------------------------------------------------------------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i16x4 lds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(const_cast<uint16_t*>(p)));
+}
+
+// Per-lane element offset of the transpose read for k0 = n0 = 0 (add k0 * pitch + n0).
+__device__ __forceinline__ int tr_lane_offset(int pitch) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;   // 16-lane group
+    const int kq = lane & 15;  // lane inside the group
+    const int row = 4 * (lane >> 5) + (kq >> 2);
+    const int col = 16 * (g & 1) + 4 * (kq & 3);
+    return row * pitch + col;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag read_tr_frag(const uint16_t* lds_lane,
+                                                               int pitch) {
+    const i16x4 lo = lds_read_tr16(lds_lane);
+    const i16x4 hi = lds_read_tr16(lds_lane + 8 * pitch);
+    u32x4 v;
+    v[0] = __builtin_bit_cast(u32x2, lo)[0];
+    v[1] = __builtin_bit_cast(u32x2, lo)[1];
+    v[2] = __builtin_bit_cast(u32x2, hi)[0];
+    v[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_frag<T>(v);
+}
+
+// ---------------------------------------------------------------------------------------------
+// MFMA policy: one interface over v_mfma_f32_32x32x16_{bf16,f16} (k = 16 per instruction) and
+// v_mfma_f32_32x32x2f32 (k = 2), so a kernel is written once for all three element types.
+//   row_operand(p): operand whose k index runs along a row of a row-major matrix; p points at
+//                   element k0 of this lane's row. Lane half h supplies k = k0 + kslot_row(h, .).
+//   acc_operand(c, j): step j of a 32-row accumulator tile reused as an operand (k = tile rows).
+//   col_operand(tile, j, pitch): operand whose k index runs down the rows of a row-major LDS
+//                   tile (32 rows); `tile` already includes this lane's column offset and, for
+//                   16-bit types, the transpose-read lane offset (tr_lane_offset).
+//   kSteps = 32 / KW MFMAs contract one 32-row tile.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+struct Mma {
+    using elem = uint16_t;
+    using frag = typename Elem<T>::frag;
+    static constexpr int KW = 16;
+    static constexpr int kSteps = 2;
+    static __device__ __forceinline__ frag zero() { return as_frag<T>(u32x4{0u, 0u, 0u, 0u}); }
+    static __device__ __forceinline__ frag row_operand(const elem* p) {
+        return as_frag<T>(ld16(p + 8 * ((threadIdx.x & 63) >> 5)));
+    }
+    static __device__ __forceinline__ frag acc_operand(const f32x16& c, int j) {
+        return pack_frag<T>(c[8 * j + 0], c[8 * j + 1], c[8 * j + 2], c[8 * j + 3], c[8 * j + 4],
+                            c[8 * j + 5], c[8 * j + 6], c[8 * j + 7]);
+    }
+    // `tile` = tile base + tr_lane_offset(pitch) + column offset.
+    static __device__ __forceinline__ frag col_operand(const elem* tile, int j, int pitch) {
+        return read_tr_frag<T>(tile + 16 * j * pitch, pitch);
+    }
+    static __device__ __forceinline__ int col_lane_offset(int pitch) {
+        return tr_lane_offset(pitch);
+    }
+    static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+        return Elem<T>::mma(a, b, c);
+    }
+};
+
+template <>
+struct Mma<float> {
+    using elem = float;
+    using frag = float;
+    static constexpr int KW = 2;
+    static constexpr int kSteps = 16;
+    static __device__ __forceinline__ frag zero() { return 0.0f; }
+    static __device__ __forceinline__ frag row_operand(const elem* p) {
+        return p[(threadIdx.x & 63) >> 5];
+    }
+    static __device__ __forceinline__ frag acc_operand(const f32x16& c, int j) { return c[j]; }
+    // `tile` = tile base + col_lane_offset(pitch) + column offset; step j reads tile row
+    // 8*(j/4) + 4*h + j%4 (h = lane half), the accumulator row held in register j.
+    static __device__ __forceinline__ frag col_operand(const elem* tile, int j, int pitch) {
+        return tile[(8 * (j >> 2) + (j & 3)) * pitch];
+    }
+    static __device__ __forceinline__ int col_lane_offset(int pitch) {
+        const int lane = threadIdx.x & 63;
+        return 4 * (lane >> 5) * pitch + (lane & 31);
+    }
+    static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+        return mma_f32(a, b, c);
+    }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Wave reductions
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float xor_shuffle(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------------------------
+// Workgroup scheduling.
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X (workgroup i -> XCD i % 8),
+// and each XCD has its own L2. `xcd_remap` renumbers dispatch slots so that consecutive logical
+// ids land on the same XCD: the blocks of one (batch, head) share K/V in one L2.
+// ---------------------------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    if (nblocks % kNumXcd != 0) return bid;
+    const int per_xcd = nblocks / kNumXcd;
+    return (bid % kNumXcd) * per_xcd + bid / kNumXcd;
+}
+
+}  // namespace dev
+}  // namespace cuflash

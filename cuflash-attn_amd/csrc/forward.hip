@@ -1,0 +1,416 @@
+// FlashAttention forward for gfx950 (MI355X).
+//
+// Replaces the reference's scalar forward kernel (src/forward/flash_attention_forward_typed.cu
+// :16-152) and its WMMA kernel (src/forward/flash_attention_forward_wmma.cu:30-207) with two
+// MFMA kernels of the same math:
+//   fwd16_kernel<T, D>: fp16 / bf16 inputs on v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate.
+//                       P is rounded to T before P*V while the row sum uses the fp32 P, as in the
+//                       reference WMMA kernel (forward_wmma.cu:151-156).
+//   fwd32_kernel<D>:    fp32 inputs on v_mfma_f32_32x32x2f32 (full fp32 products), P kept fp32
+//                       as in the reference scalar kernel (forward_typed.cu:113-129).
+//
+// Work decomposition (both kernels): one workgroup = 4 waves = 128 query rows of one
+// (batch, head); each wave owns 32 query rows. The kernel streams key/value blocks through LDS;
+// per block each wave computes S^T = K Q^T (A = K tile from LDS, B = Q^T held in registers for
+// the whole kernel), runs the online softmax on the accumulator tile in place, and accumulates
+// O^T += V^T P^T (A = V tile read with LDS transpose reads, B = P straight from the score
+// registers). Each lane therefore owns one query row of O, and the softmax rescale is a per-lane
+// multiply. The next K/V block is fetched into registers while the current one is consumed.
+// Causal launches process the longest query blocks first; blocks of one head share an XCD.
+
+#include "common.hpp"
+#include "launch.hpp"
+#include "softmax.hpp"
+
+namespace cuflash {
+namespace dev {
+
+// ------------------------------------------------------------------------------------------
+// fp16 / bf16 kernel
+// ------------------------------------------------------------------------------------------
+template <int D>
+struct Fwd16Cfg {
+    static constexpr int kThreads = 256;
+    static constexpr int BM = 128;  // query rows per workgroup (32 per wave)
+    static constexpr int BN = 64;   // keys per LDS block
+    // K tile pitch: consecutive rows start 16 bytes apart modulo 256 bytes, so the 16-byte row
+    // reads of an S^T operand (32 rows, same column) are bank-conflict free.
+    static constexpr int KP = D + 8;
+    // V tile pitch: consecutive rows start 64 bytes apart modulo 128 bytes, so the 8 rows x 64
+    // bytes touched by one transpose read spread evenly over the banks.
+    static constexpr int VP = ((2 * D) % 128 == 64) ? D : D + 32;
+    static constexpr int kChunksPerRow = D / 8;  // 16-byte chunks per row
+    static constexpr int kChunksPerThread = BN * kChunksPerRow / kThreads;
+    static_assert(BN * kChunksPerRow % kThreads == 0, "tile copy must divide evenly");
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 2)
+    fwd16_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                 const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ L,
+                 int N, int nqb, float c, int causal) {
+    using Cfg = Fwd16Cfg<D>;
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[Cfg::BN * Cfg::KP];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[Cfg::BN * Cfg::VP];
+
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lid / nqb;
+    const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * N * D;
+    const uint16_t* Qh = Q + head;
+    const uint16_t* Kh = K + head;
+    const uint16_t* Vh = V + head;
+
+    const int q0 = qb * Cfg::BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;                   // query row owned by this lane
+
+    // Q^T as the B operand of S^T = K Q^T: lane holds Q[q][16*ks + 8*g2 + 0..7].
+    frag qf[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < N) v = ld16(Qh + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;
+    float l = 0.0f;
+
+    const int kv_end = causal ? min(N, (qb + 1) * Cfg::BM) : N;
+    const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
+
+    u32x4 kreg[Cfg::kChunksPerThread];
+    u32x4 vreg[Cfg::kChunksPerThread];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
+            const int id = i * Cfg::kThreads + tid;
+            const int row = id / Cfg::kChunksPerRow;
+            const int col = (id % Cfg::kChunksPerRow) * 8;
+            const int key = kb * Cfg::BN + row;
+            if (key < N) {
+                const size_t off = static_cast<size_t>(key) * D + col;
+                kreg[i] = ld16(Kh + off);
+                vreg[i] = ld16(Vh + off);
+            } else {
+                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+                vreg[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
+            const int id = i * Cfg::kThreads + tid;
+            const int row = id / Cfg::kChunksPerRow;
+            const int col = (id % Cfg::kChunksPerRow) * 8;
+            st16(&Ks[row * Cfg::KP + col], kreg[i]);
+            st16(&Vs[row * Cfg::VP + col], vreg[i]);
+        }
+    };
+
+    const int tr_off = tr_lane_offset(Cfg::VP);
+    if (nkb > 0) fetch(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        __syncthreads();  // every wave is done reading the previous block
+        stage();
+        __syncthreads();
+        if (kb + 1 < nkb) fetch(kb + 1);
+
+        const int key0 = kb * Cfg::BN;
+        if (causal && key0 > q0 + 31) continue;  // whole block lies in this wave's future
+
+        // S^T = K Q^T for the two 32-key tiles of the block.
+        f32x16 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+                const frag a =
+                    as_frag<T>(ld16(&Ks[(32 * t + l32) * Cfg::KP + 16 * ks + 8 * g2]));
+                s[t] = Elem<T>::mma(a, qf[ks], s[t]);
+            }
+        }
+
+        const bool masked = (key0 + Cfg::BN > N) || (causal && key0 + Cfg::BN - 1 > q0);
+        float alpha;
+        const bool rescale =
+            masked ? softmax_step<2, true>(s, key0, q, N, causal != 0, c, m, l, alpha)
+                   : softmax_step<2, false>(s, key0, q, N, causal != 0, c, m, l, alpha);
+        if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+
+        // O^T += V^T P^T in four 16-key steps.
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = j >> 1;
+            const int h = j & 1;
+            const frag p = pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2],
+                                        s[t][8 * h + 3], s[t][8 * h + 4], s[t][8 * h + 5],
+                                        s[t][8 * h + 6], s[t][8 * h + 7]);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const frag a = read_tr_frag<T>(&Vs[16 * j * Cfg::VP + 32 * dt + tr_off], Cfg::VP);
+                o[dt] = Elem<T>::mma(a, p, o[dt]);
+            }
+        }
+    }
+
+    // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
+    l += xor_shuffle(l, 32);
+    if (q < N) {
+        const float inv = 1.0f / l;
+        uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                u32x2 w;
+                w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
+                w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
+                st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// fp32 kernel
+// ------------------------------------------------------------------------------------------
+template <int D>
+struct Fwd32Cfg {
+    static constexpr int kThreads = 256;
+    static constexpr int BM = 128;
+    static constexpr int BN = 32;
+    static constexpr int KP = D + 4;  // rows 16 bytes apart modulo 256 bytes
+    static constexpr int VP = D + 8;  // the two rows read by one instruction sit 128 bytes apart
+    static constexpr int kChunksPerRow = D / 4;
+    static constexpr int kChunksPerThread = BN * kChunksPerRow / kThreads;
+    static_assert(BN * kChunksPerRow % kThreads == 0, "tile copy must divide evenly");
+};
+
+template <int D>
+__global__ void __launch_bounds__(256, 2)
+    fwd32_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                 const float* __restrict__ V, float* __restrict__ O, float* __restrict__ L, int N,
+                 int nqb, float c, int causal) {
+    using Cfg = Fwd32Cfg<D>;
+    __shared__ __attribute__((aligned(16))) float Ks[Cfg::BN * Cfg::KP];
+    __shared__ __attribute__((aligned(16))) float Vs[Cfg::BN * Cfg::VP];
+
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = lid / nqb;
+    const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * N * D;
+    const float* Qh = Q + head;
+    const float* Kh = K + head;
+    const float* Vh = V + head;
+    const int q0 = qb * Cfg::BM + wave * 32;
+    const int q = q0 + l32;
+
+    // Q^T operand: the k index of MFMA step ks in lane half g2 is d = (D/2)*g2 + ks.
+    float qf[D / 2];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (q < N) v = __builtin_bit_cast(f32x4, ld16(Qh + static_cast<size_t>(q) * D + (D / 2) * g2 + 4 * i));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) qf[4 * i + u] = v[u];
+    }
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;
+    float l = 0.0f;
+
+    const int kv_end = causal ? min(N, (qb + 1) * Cfg::BM) : N;
+    const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
+
+    u32x4 kreg[Cfg::kChunksPerThread];
+    u32x4 vreg[Cfg::kChunksPerThread];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
+            const int id = i * Cfg::kThreads + tid;
+            const int row = id / Cfg::kChunksPerRow;
+            const int col = (id % Cfg::kChunksPerRow) * 4;
+            const int key = kb * Cfg::BN + row;
+            if (key < N) {
+                const size_t off = static_cast<size_t>(key) * D + col;
+                kreg[i] = ld16(Kh + off);
+                vreg[i] = ld16(Vh + off);
+            } else {
+                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+                vreg[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
+            const int id = i * Cfg::kThreads + tid;
+            const int row = id / Cfg::kChunksPerRow;
+            const int col = (id % Cfg::kChunksPerRow) * 4;
+            st16(&Ks[row * Cfg::KP + col], kreg[i]);
+            st16(&Vs[row * Cfg::VP + col], vreg[i]);
+        }
+    };
+
+    if (nkb > 0) fetch(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (kb + 1 < nkb) fetch(kb + 1);
+
+        const int key0 = kb * Cfg::BN;
+        if (causal && key0 > q0 + 31) continue;
+
+        f32x16 s[1];
+        s[0] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            const f32x4 a4 = __builtin_bit_cast(
+                f32x4, ld16(&Ks[l32 * Cfg::KP + (D / 2) * g2 + 4 * i]));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) s[0] = mma_f32(a4[u], qf[4 * i + u], s[0]);
+        }
+
+        const bool masked = (key0 + Cfg::BN > N) || (causal && key0 + Cfg::BN - 1 > q0);
+        float alpha;
+        const bool rescale =
+            masked ? softmax_step<1, true>(s, key0, q, N, causal != 0, c, m, l, alpha)
+                   : softmax_step<1, false>(s, key0, q, N, causal != 0, c, m, l, alpha);
+        if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+
+        // O^T += V^T P^T: step r contracts the two keys 8*(r/4) + 4*h + r%4 (h = lane half).
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = 8 * (r >> 2) + 4 * g2 + (r & 3);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const float a = Vs[key * Cfg::VP + 32 * dt + l32];
+                o[dt] = mma_f32(a, s[0][r], o[dt]);
+            }
+        }
+    }
+
+    l += xor_shuffle(l, 32);
+    if (q < N) {
+        const float inv = 1.0f / l;
+        float* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                f32x4 w;
+                w[0] = o[dt][4 * a + 0] * inv;
+                w[1] = o[dt][4 * a + 1] * inv;
+                w[2] = o[dt][4 * a + 2] * inv;
+                w[3] = o[dt][4 * a + 3] * inv;
+                st16(Orow + 32 * dt + 8 * a + 4 * g2, __builtin_bit_cast(u32x4, w));
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
+}  // namespace dev
+
+namespace detail {
+
+namespace {
+
+template <typename T, int D>
+FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, float* L, int BH,
+                                  int N, float scale, bool causal, hipStream_t stream) {
+    using Cfg = dev::Fwd16Cfg<D>;
+    const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
+    const long long blocks = static_cast<long long>(nqb) * BH;
+    if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+                       reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
+                       reinterpret_cast<uint16_t*>(O), L, N, nqb, scale * dev::kLog2e,
+                       causal ? 1 : 0);
+    return from_hip(hipGetLastError());
+}
+
+template <int D>
+FlashAttentionError run_forward32(const float* Q, const float* K, const float* V, float* O,
+                                  float* L, int BH, int N, float scale, bool causal,
+                                  hipStream_t stream) {
+    using Cfg = dev::Fwd32Cfg<D>;
+    const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
+    const long long blocks = static_cast<long long>(nqb) * BH;
+    if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    hipLaunchKernelGGL((dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, N, nqb,
+                       scale * dev::kLog2e, causal ? 1 : 0);
+    return from_hip(hipGetLastError());
+}
+
+}  // namespace
+
+template <typename T>
+FlashAttentionError launch_forward(const T* Q, const T* K, const T* V, T* O, float* L,
+                                   int batch_size, int num_heads, int seq_len, int head_dim,
+                                   float scale, bool causal, hipStream_t stream) {
+    const long long bh = static_cast<long long>(batch_size) * num_heads;
+    if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const int BH = static_cast<int>(bh);
+    if constexpr (std::is_same<T, float>::value) {
+        switch (head_dim) {
+            case 32: return run_forward32<32>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+            case 64: return run_forward32<64>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+            case 128: return run_forward32<128>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+        }
+    } else {
+        switch (head_dim) {
+            case 32: return run_forward16<T, 32>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+            case 64: return run_forward16<T, 64>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+            case 128:
+                return run_forward16<T, 128>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
+        }
+    }
+    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+}
+
+template FlashAttentionError launch_forward<float>(const float*, const float*, const float*,
+                                                   float*, float*, int, int, int, int, float, bool,
+                                                   hipStream_t);
+template FlashAttentionError launch_forward<__half>(const __half*, const __half*, const __half*,
+                                                    __half*, float*, int, int, int, int, float,
+                                                    bool, hipStream_t);
+template FlashAttentionError launch_forward<__hip_bfloat16>(const __hip_bfloat16*,
+                                                            const __hip_bfloat16*,
+                                                            const __hip_bfloat16*,
+                                                            __hip_bfloat16*, float*, int, int, int,
+                                                            int, float, bool, hipStream_t);
+
+}  // namespace detail
+}  // namespace cuflash

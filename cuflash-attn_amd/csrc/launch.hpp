@@ -1,0 +1,70 @@
+#pragma once
+
+// Internal launcher interface between the validating API layer (api.cpp) and the gfx950
+// kernels (forward.hip, backward.hip, decode.hip). Arguments have already been validated when a
+// launcher runs; launchers only check the HIP runtime.
+
+#include "cuflash/flash_attention.h"
+
+namespace cuflash {
+namespace detail {
+
+// Counterpart of the reference's launch_flash_attention_forward_typed<T>
+// (src/forward/flash_attention_forward_typed.cu:212-302).
+template <typename T>
+FlashAttentionError launch_forward(const T* Q, const T* K, const T* V, T* O, float* L,
+                                   int batch_size, int num_heads, int seq_len, int head_dim,
+                                   float scale, bool causal, hipStream_t stream);
+
+// Counterpart of the reference's launch_flash_attention_backward_typed<T>
+// (src/backward/flash_attention_backward_typed.cu:440-579).
+template <typename T>
+FlashAttentionError launch_backward(const T* Q, const T* K, const T* V, const T* O,
+                                    const float* L, const T* dO, T* dQ, T* dK, T* dV,
+                                    int batch_size, int num_heads, int seq_len, int head_dim,
+                                    float scale, bool causal, hipStream_t stream);
+
+// Split-KV decode (no reference counterpart).
+template <typename T>
+FlashAttentionError launch_decode(const T* Q, const T* K, const T* V, T* O, float* L,
+                                  int batch_size, int num_heads, int kv_len, int head_dim,
+                                  float scale, int num_splits, hipStream_t stream);
+
+// Maps a HIP status after a launch or allocation to the library's error code.
+inline FlashAttentionError from_hip(hipError_t e) {
+    if (e == hipSuccess) return FlashAttentionError::SUCCESS;
+    if (e == hipErrorOutOfMemory) return FlashAttentionError::OUT_OF_MEMORY;
+    return FlashAttentionError::CUDA_ERROR;
+}
+
+// Stream-ordered device workspace (hipMallocAsync / hipFreeAsync on the caller's stream), the
+// counterpart of the reference's AsyncFloatBuffer (src/backward/flash_attention_backward_typed.cu
+// :374-394). Freed in stream order when the launcher returns, so the host never synchronizes and
+// concurrent calls on different streams never share memory.
+class StreamWorkspace {
+public:
+    explicit StreamWorkspace(hipStream_t stream) : stream_(stream) {}
+    StreamWorkspace(const StreamWorkspace&) = delete;
+    StreamWorkspace& operator=(const StreamWorkspace&) = delete;
+    ~StreamWorkspace() {
+        if (ptr_) (void)hipFreeAsync(ptr_, stream_);
+    }
+    FlashAttentionError alloc(size_t bytes) {
+        hipError_t e = hipMallocAsync(&ptr_, bytes, stream_);
+        if (e != hipSuccess) {
+            ptr_ = nullptr;
+            (void)hipGetLastError();
+            return e == hipErrorOutOfMemory ? FlashAttentionError::OUT_OF_MEMORY
+                                            : FlashAttentionError::CUDA_ERROR;
+        }
+        return FlashAttentionError::SUCCESS;
+    }
+    void* get() const { return ptr_; }
+
+private:
+    hipStream_t stream_;
+    void* ptr_ = nullptr;
+};
+
+}  // namespace detail
+}  // namespace cuflash

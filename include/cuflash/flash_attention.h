@@ -1,0 +1,186 @@
+#pragma once
+
+// Public API of libcuflash_attn for AMD Instinct MI355X (gfx950).
+//
+// Drop-in for the reference's include/cuflash/flash_attention.h:
+//   - same namespace, enum, enum values and order (SUCCESS=0 ... UNSUPPORTED_DTYPE=7),
+//     reference flash_attention.h:12-21;
+//   - same C++ overload set (float / half / bfloat16; L is always float*),
+//     reference flash_attention.h:30-71;
+//   - same C ABI names and argument order, reference flash_attention.h:81-118.
+// CUDA types map to their HIP equivalents: half -> __half (hip_fp16.h),
+// __nv_bfloat16 -> __hip_bfloat16 (hip_bf16.h), cudaStream_t -> hipStream_t. The C ABI is
+// binary-identical for ctypes callers (every tensor is an opaque device pointer and the stream
+// is an opaque pointer); the C++ overloads are source-compatible.
+//
+// Layout: every tensor is a contiguous row-major [batch_size, num_heads, seq_len, head_dim]
+// device buffer; L is [batch_size, num_heads, seq_len] float. All work is enqueued on `stream`
+// and nothing synchronizes the host; kernel execution errors surface at the caller's next
+// synchronizing call, as in the reference.
+//
+// Additive entry points (no counterpart in the reference, which lists split-KV decoding as a
+// roadmap item, ROADMAP.md:24-25): flash_attention_decode / cuflash_attention_decode_*.
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "cuflash/export.h"
+
+namespace cuflash {
+
+// Error codes. Values and order are part of the ABI (reference flash_attention.h:12-21).
+enum class FlashAttentionError {
+    SUCCESS = 0,
+    INVALID_DIMENSION,     // a dimension is <= 0, or scale is NaN/Inf/negative
+    DIMENSION_MISMATCH,    // declared for compatibility; never returned
+    NULL_POINTER,          // an input or output pointer is null
+    CUDA_ERROR,            // the HIP runtime reported an error (launch or allocation)
+    OUT_OF_MEMORY,         // the backward/decode workspace could not be allocated
+    UNSUPPORTED_HEAD_DIM,  // head_dim is not 32, 64 or 128
+    UNSUPPORTED_DTYPE      // declared for compatibility; never returned
+};
+
+// Fixed English message per error code (reference src/api/flash_attention_api.cu:21-42).
+CUFLASH_EXPORT const char* get_error_string(FlashAttentionError error);
+
+// ---- Forward: O = softmax(scale * Q K^T [+ causal mask]) V,  L = logsumexp of each row ----
+// Reference: include/cuflash/flash_attention.h:30-34 (float), :48-52 (half), :60-65 (bf16).
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward(const float* Q, const float* K,
+                                                           const float* V, float* O, float* L,
+                                                           int batch_size, int num_heads,
+                                                           int seq_len, int head_dim, float scale,
+                                                           bool causal, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward(const __half* Q, const __half* K,
+                                                           const __half* V, __half* O, float* L,
+                                                           int batch_size, int num_heads,
+                                                           int seq_len, int head_dim, float scale,
+                                                           bool causal, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V, __hip_bfloat16* O,
+    float* L, int batch_size, int num_heads, int seq_len, int head_dim, float scale, bool causal,
+    hipStream_t stream = 0);
+
+// ---- Backward: dQ, dK, dV from Q, K, V, O, L (fp32 logsumexp) and dO ----
+// dQ/dK/dV are overwritten. Reference: include/cuflash/flash_attention.h:37-40, :54-57, :67-71.
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward(
+    const float* Q, const float* K, const float* V, const float* O, const float* L, const float* dO,
+    float* dQ, float* dK, float* dV, int batch_size, int num_heads, int seq_len, int head_dim,
+    float scale, bool causal, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward(
+    const __half* Q, const __half* K, const __half* V, const __half* O, const float* L,
+    const __half* dO, __half* dQ, __half* dK, __half* dV, int batch_size, int num_heads,
+    int seq_len, int head_dim, float scale, bool causal, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    const __hip_bfloat16* O, const float* L, const __hip_bfloat16* dO, __hip_bfloat16* dQ,
+    __hip_bfloat16* dK, __hip_bfloat16* dV, int batch_size, int num_heads, int seq_len,
+    int head_dim, float scale, bool causal, hipStream_t stream = 0);
+
+// ---- Split-KV decode (additive; no reference counterpart, see ROADMAP.md:24-25) ----
+// One query row per (batch, head) attends to kv_len keys, non-causal:
+//   Q, O: [batch_size, num_heads, 1, head_dim]; K, V: [batch_size, num_heads, kv_len, head_dim];
+//   L: [batch_size, num_heads] float logsumexp.
+// The keys are cut into num_splits chunks; each chunk yields an unnormalized partial (O_s, m_s,
+// l_s) in a stream-ordered workspace and a second kernel merges them with the online-softmax
+// rule. num_splits == 0 picks a split count from the device's CU count; larger values than
+// ceil(kv_len / 16) or 1024 are reduced to that. num_splits < 0 is INVALID_DIMENSION.
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode(const float* Q, const float* K,
+                                                          const float* V, float* O, float* L,
+                                                          int batch_size, int num_heads,
+                                                          int kv_len, int head_dim, float scale,
+                                                          int num_splits, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode(const __half* Q, const __half* K,
+                                                          const __half* V, __half* O, float* L,
+                                                          int batch_size, int num_heads,
+                                                          int kv_len, int head_dim, float scale,
+                                                          int num_splits, hipStream_t stream = 0);
+
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V, __hip_bfloat16* O,
+    float* L, int batch_size, int num_heads, int kv_len, int head_dim, float scale,
+    int num_splits, hipStream_t stream = 0);
+
+}  // namespace cuflash
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Stable C ABI. Return values are the integer value of cuflash::FlashAttentionError.
+// Each declaration replaces the reference symbol of the same name
+// (include/cuflash/flash_attention.h:81-118; defined at src/api/flash_attention_api.cu:188-240).
+
+// Replaces reference flash_attention.h:83-86.
+CUFLASH_EXPORT int cuflash_attention_forward_f32(const float* Q, const float* K, const float* V,
+                                                 float* O, float* L, int batch_size, int num_heads,
+                                                 int seq_len, int head_dim, float scale,
+                                                 bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:88-92.
+CUFLASH_EXPORT int cuflash_attention_backward_f32(const float* Q, const float* K, const float* V,
+                                                  const float* O, const float* L, const float* dO,
+                                                  float* dQ, float* dK, float* dV, int batch_size,
+                                                  int num_heads, int seq_len, int head_dim,
+                                                  float scale, bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:94-97.
+CUFLASH_EXPORT int cuflash_attention_forward_f16(const __half* Q, const __half* K, const __half* V,
+                                                 __half* O, float* L, int batch_size,
+                                                 int num_heads, int seq_len, int head_dim,
+                                                 float scale, bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:99-103.
+CUFLASH_EXPORT int cuflash_attention_backward_f16(const __half* Q, const __half* K,
+                                                  const __half* V, const __half* O, const float* L,
+                                                  const __half* dO, __half* dQ, __half* dK,
+                                                  __half* dV, int batch_size, int num_heads,
+                                                  int seq_len, int head_dim, float scale,
+                                                  bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:105-109.
+CUFLASH_EXPORT int cuflash_attention_forward_bf16(const __hip_bfloat16* Q,
+                                                  const __hip_bfloat16* K,
+                                                  const __hip_bfloat16* V, __hip_bfloat16* O,
+                                                  float* L, int batch_size, int num_heads,
+                                                  int seq_len, int head_dim, float scale,
+                                                  bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:111-116.
+CUFLASH_EXPORT int cuflash_attention_backward_bf16(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    const __hip_bfloat16* O, const float* L, const __hip_bfloat16* dO, __hip_bfloat16* dQ,
+    __hip_bfloat16* dK, __hip_bfloat16* dV, int batch_size, int num_heads, int seq_len,
+    int head_dim, float scale, bool causal, hipStream_t stream);
+
+// Replaces reference flash_attention.h:119 (cuflash_error_string).
+CUFLASH_EXPORT const char* cuflash_error_string(int error_code);
+
+// Additive split-KV decode ABI (no reference counterpart; ROADMAP.md:24-25 lists it as planned).
+CUFLASH_EXPORT int cuflash_attention_decode_f32(const float* Q, const float* K, const float* V,
+                                                float* O, float* L, int batch_size, int num_heads,
+                                                int kv_len, int head_dim, float scale,
+                                                int num_splits, hipStream_t stream);
+
+CUFLASH_EXPORT int cuflash_attention_decode_f16(const __half* Q, const __half* K, const __half* V,
+                                                __half* O, float* L, int batch_size,
+                                                int num_heads, int kv_len, int head_dim,
+                                                float scale, int num_splits, hipStream_t stream);
+
+CUFLASH_EXPORT int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const __hip_bfloat16* K,
+                                                 const __hip_bfloat16* V, __hip_bfloat16* O,
+                                                 float* L, int batch_size, int num_heads,
+                                                 int kv_len, int head_dim, float scale,
+                                                 int num_splits, hipStream_t stream);
+
+// Library version string (CUFLASH_VERSION); additive.
+CUFLASH_EXPORT const char* cuflash_version(void);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,159 @@
+"""C-ABI boundary checks that need no GPU.
+
+Mirrors the host-only parts of the reference's tests: tests/integration/test_api_smoke.cpp:11-41
+(validation errors returned before any device work), tests/unit/test_error_handling.cu:21-253
+(error codes and exact strings) and tests/unit/test_stress_edge_cases.cu:124-175. Every call
+here fails validation, so the library returns before its first HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+
+import pytest
+
+import cuflash_attn
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "cuflash", "flash_attention.h")
+
+
+def _declared_c_symbols():
+    text = open(HEADER).read()
+    c_part = text[text.index('extern "C"'):]
+    return sorted(set(re.findall(r"CUFLASH_EXPORT\s+[\w\s\*]+?\b(cuflash_\w+)\s*\(", c_part)))
+
+
+def test_library_loads_from_reference_search_path(lib):
+    assert lib.path.endswith(os.path.join("build", "libcuflash_attn.so"))
+    assert lib.version() == "0.6.0"
+
+
+def test_every_declared_symbol_is_exported(lib):
+    declared = _declared_c_symbols()
+    assert len(declared) == 11, declared
+    out = subprocess.run(["nm", "-D", "--defined-only", lib.path], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for sym in declared:
+        assert sym in exported, sym
+        assert getattr(lib.library, sym) is not None
+    assert set(declared) == set(cuflash_attn.EXPORTED_SYMBOLS)
+
+
+def test_only_the_public_api_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", lib.path], capture_output=True,
+                         text=True, check=True).stdout
+    names = [line.split(" ", 2)[-1] for line in out.splitlines() if " T " in line]
+    for n in names:
+        assert n.startswith("cuflash"), n  # C ABI or the cuflash:: C++ API, nothing internal
+
+
+# Reference src/api/flash_attention_api.cu:21-42, checked verbatim by test_error_handling.cu:236-250.
+EXPECTED_STRINGS = {
+    0: "Success",
+    1: "Invalid dimension: dimensions must be positive",
+    2: "Dimension mismatch: Q, K, V tensors have incompatible shapes",
+    3: "Null pointer: input or output pointer is null",
+    4: "CUDA error occurred",
+    5: "Out of memory: insufficient GPU memory",
+    6: "Unsupported head_dim: must be 32, 64, or 128",
+    7: "Unsupported data type",
+    8: "Unknown error",
+    -1: "Unknown error",
+}
+
+
+@pytest.mark.parametrize("code", sorted(EXPECTED_STRINGS))
+def test_error_strings(lib, code):
+    assert lib.error_string(code) == EXPECTED_STRINGS[code]
+
+
+# Host buffers stand in for device pointers: validation never dereferences them.
+_BUF = (ctypes.c_float * 16)()
+P = ctypes.addressof(_BUF)
+
+
+def _fwd(lib, sfx, ptrs, b=1, h=1, n=16, d=32, scale=1.0, causal=False):
+    return lib.fn("forward", sfx)(*ptrs, b, h, n, d, scale, causal, None)
+
+
+def _bwd(lib, sfx, ptrs, b=1, h=1, n=16, d=32, scale=1.0, causal=False):
+    return lib.fn("backward", sfx)(*ptrs, b, h, n, d, scale, causal, None)
+
+
+@pytest.mark.parametrize("sfx", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("null_idx", range(5))
+def test_forward_null_pointers(lib, sfx, null_idx):
+    ptrs = [P] * 5
+    ptrs[null_idx] = None
+    assert _fwd(lib, sfx, ptrs) == cuflash_attn.NULL_POINTER
+
+
+@pytest.mark.parametrize("sfx", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("null_idx", range(9))
+def test_backward_null_pointers(lib, sfx, null_idx):
+    ptrs = [P] * 9
+    ptrs[null_idx] = None
+    assert _bwd(lib, sfx, ptrs) == cuflash_attn.NULL_POINTER
+
+
+@pytest.mark.parametrize("dims", [(0, 1, 16, 32), (-1, 1, 16, 32), (1, 0, 16, 32),
+                                  (1, 1, 0, 32), (1, 1, 16, 0), (1, 1, -5, 64)])
+@pytest.mark.parametrize("sfx", ["f32", "f16", "bf16"])
+def test_invalid_dimensions(lib, sfx, dims):
+    b, h, n, d = dims
+    assert _fwd(lib, sfx, [P] * 5, b, h, n, d) == cuflash_attn.INVALID_DIMENSION
+    assert _bwd(lib, sfx, [P] * 9, b, h, n, d) == cuflash_attn.INVALID_DIMENSION
+
+
+@pytest.mark.parametrize("d", [48, 256, 16, 96, 1])
+def test_unsupported_head_dim(lib, d):
+    for sfx in ("f32", "f16", "bf16"):
+        assert _fwd(lib, sfx, [P] * 5, d=d) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+        assert _bwd(lib, sfx, [P] * 9, d=d) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+
+
+@pytest.mark.parametrize("scale", [math.nan, math.inf, -math.inf, -1.0, -1e-30])
+def test_invalid_scale(lib, scale):
+    for sfx in ("f32", "f16", "bf16"):
+        assert _fwd(lib, sfx, [P] * 5, scale=scale) == cuflash_attn.INVALID_DIMENSION
+        assert _bwd(lib, sfx, [P] * 9, scale=scale) == cuflash_attn.INVALID_DIMENSION
+
+
+def test_validation_order_matches_reference(lib):
+    # null beats bad dims (flash_attention_api.cu:49-55)
+    assert _fwd(lib, "f32", [None] + [P] * 4, b=0) == cuflash_attn.NULL_POINTER
+    # bad dims beat bad head_dim (:53-59)
+    assert _fwd(lib, "f32", [P] * 5, b=0, d=48) == cuflash_attn.INVALID_DIMENSION
+    # bad head_dim beats bad scale (:57-63)
+    assert _fwd(lib, "f32", [P] * 5, d=48, scale=math.nan) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+    # backward checks gradient pointers before the forward-side ones (:74-78)
+    assert _bwd(lib, "f32", [None] * 9, d=48) == cuflash_attn.NULL_POINTER
+    assert _bwd(lib, "f32", [P] * 5 + [None] + [P] * 3, b=-1) == cuflash_attn.NULL_POINTER
+
+
+def test_decode_validation(lib):
+    dec = lib.fn("decode", "f16")
+    assert dec(None, P, P, P, P, 1, 1, 16, 32, 1.0, 0, None) == cuflash_attn.NULL_POINTER
+    assert dec(P, P, P, P, P, 1, 1, 0, 32, 1.0, 0, None) == cuflash_attn.INVALID_DIMENSION
+    assert dec(P, P, P, P, P, 1, 1, 16, 48, 1.0, 0, None) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+    assert dec(P, P, P, P, P, 1, 1, 16, 32, math.nan, 0, None) == cuflash_attn.INVALID_DIMENSION
+    assert dec(P, P, P, P, P, 1, 1, 16, 32, 1.0, -1, None) == cuflash_attn.INVALID_DIMENSION
+
+
+def test_candidate_paths_follow_reference_order(monkeypatch):
+    monkeypatch.setenv("CUFLASH_LIB", "/nonexistent/libcuflash_attn.so")
+    paths = cuflash_attn.candidate_library_paths()
+    assert paths[0] == "/nonexistent/libcuflash_attn.so"
+    assert paths[1] == os.path.join(REPO, "build", "libcuflash_attn.so")
+    assert paths[2].endswith(os.path.join("build", "default", "libcuflash_attn.so"))
+
+
+def test_missing_library_fails_loudly():
+    with pytest.raises(OSError):
+        cuflash_attn.load_library("/nonexistent/libcuflash_attn.so")

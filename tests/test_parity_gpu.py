@@ -1,0 +1,102 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the fp64 CPU oracle.
+
+Tolerances (north star): FP32 O and L within 1e-4 relative (max |diff| / max |ref|);
+FP16/BF16 O, L, dQ, dK, dV within 2e-2 max-abs. The oracle runs on the same rounded inputs.
+FP32 gradients are held to 1e-4 relative as well (the reference's own fp32 backward test uses
+1e-3 absolute, tests/unit/test_backward.cu:202-204).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import cuflash_attn
+import oracle
+from conftest import max_abs
+from cuflash_attn import synth
+
+DTYPES = ["float32", "float16", "bfloat16"]
+TOL_16 = 2e-2
+TOL_32 = 1e-4
+
+
+def make_inputs(shape, dtype, seeds=(1, 2, 3, 4), dist="uniform", std=1.0):
+    out = []
+    for s in seeds:
+        x = synth.uniform(s, shape) if dist == "uniform" else synth.normal(s, shape, std)
+        out.append(synth.round_to(x, dtype))
+    return out
+
+
+def check(dtype, got, ref, what):
+    if dtype == "float32":
+        # Relative to the tensor's magnitude, floored at 1e-3: an exactly-zero reference (dQ at
+        # N = 1, where dS = P (dP - D) = 0) leaves only fp32 rounding of dP - D (~1e-8).
+        err = max_abs(got, ref) / max(float(np.max(np.abs(ref))) if np.size(ref) else 0.0, 1e-3)
+        assert err <= TOL_32, f"{what}: rel err {err:.3e}"
+    else:
+        err = max_abs(got, ref)
+        assert err <= TOL_16, f"{what}: max abs err {err:.3e}"
+    return err
+
+
+def run_forward(dtype, q, k, v, scale, causal):
+    tq, tk, tv = (synth.to_torch(x, dtype) for x in (q, k, v))
+    o, lse = cuflash_attn.flash_attention_forward(tq, tk, tv, scale=scale, causal=causal)
+    return o, lse, (tq, tk, tv)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [1, 17, 128, 200])
+def test_forward_parity(torch_gpu, dtype, d, causal, n):
+    shape = (2, 3, n, d)
+    q, k, v = make_inputs(shape, dtype, seeds=(1, 2, 3))
+    scale = d ** -0.5
+    o, lse, _ = run_forward(dtype, q, k, v, scale, causal)
+    torch_gpu.cuda.synchronize()
+    o_ref, l_ref = oracle.forward(q, k, v, scale, causal)
+    check(dtype, synth.to_numpy(o), o_ref, "O")
+    check(dtype, synth.to_numpy(lse), l_ref, "L")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [1, 33, 130])
+def test_backward_parity(torch_gpu, dtype, d, causal, n):
+    shape = (1, 2, n, d)
+    q, k, v, do = make_inputs(shape, dtype)
+    scale = d ** -0.5
+    o, lse, (tq, tk, tv) = run_forward(dtype, q, k, v, scale, causal)
+    tdo = synth.to_torch(do, dtype)
+    dq, dk, dv = cuflash_attn.flash_attention_backward(tq, tk, tv, o, lse, tdo, scale=scale,
+                                                       causal=causal)
+    torch_gpu.cuda.synchronize()
+    rq, rk, rv = oracle.backward(q, k, v, do, scale, causal)
+    check(dtype, synth.to_numpy(dq), rq, "dQ")
+    check(dtype, synth.to_numpy(dk), rk, "dK")
+    check(dtype, synth.to_numpy(dv), rv, "dV")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("kv_len", [1, 100, 1000, 4099])
+@pytest.mark.parametrize("splits", [0, 1, 3, 16])
+def test_decode_parity(torch_gpu, dtype, d, kv_len, splits):
+    B, H = 2, 3
+    q = synth.round_to(synth.normal(1, (B, H, 1, d)), dtype)
+    k = synth.round_to(synth.normal(2, (B, H, kv_len, d)), dtype)
+    v = synth.round_to(synth.normal(3, (B, H, kv_len, d)), dtype)
+    scale = d ** -0.5
+    tq, tk, tv = (synth.to_torch(x, dtype) for x in (q, k, v))
+    o, lse = cuflash_attn.flash_attention_decode(tq, tk, tv, scale=scale, num_splits=splits)
+    torch_gpu.cuda.synchronize()
+    o_ref, l_ref = oracle.forward(q, k, v, scale, False)
+    check(dtype, synth.to_numpy(o), o_ref, "O")
+    check(dtype, synth.to_numpy(lse), l_ref, "L")
