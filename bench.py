@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""Headline benchmark of libcuflash_attn on one MI355X.
+
+Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM GB/s at 32k KV".
+
+* A step is one forward + one backward pass of config 3 (bf16, causal, B=2 H=16 N=4096 D=128,
+  scale 1/sqrt(128), Q/K/V/dO i.i.d. N(0,1) from seeds 1-4) on inputs resident in HBM.
+  value = (F_fwd + F_bwd) / step time with the reference's FLOP model
+  (benchmarks/bench_flash_attention.cu:34-44, causal x0.5 at :457-460):
+  F_fwd = 4 B H N^2 D / 2, F_bwd = 2.5 F_fwd.
+* Decode (config 4: fp16, B=16 H=32, 1 query, 32768 keys, D=128) is timed for 16/32/64 splits
+  and the library's automatic choice; GB/s counts K and V read once plus Q read, O and L written.
+* roofline: the dominant kernel of the step, timed live with HIP events recorded around each of
+  its launches on the launch stream (cuflash_profile_enable), against MI355X's dense bf16 MFMA
+  peak. `rooflines` lists every kernel the same way.
+* cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
+  tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
+  timed on a bounded sample of the config-3 workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "cuflash-attn_amd"))
+sys.path.insert(0, REPO)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+CFG3 = dict(B=2, H=16, N=4096, D=128, causal=True)
+CFG4 = dict(B=16, H=32, LKV=32768, D=128)
+
+
+def flops_fwd(B, H, N, D, causal):
+    return 4.0 * B * H * N * N * D * (0.5 if causal else 1.0)
+
+
+def decode_bytes(B, H, LKV, D, elem=2):
+    return B * H * D * (2 * LKV + 2) * elem + B * H * 4
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=0,
+                    help="heads in the CPU-baseline sample (default: one per host thread, <= 16)")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (every "
+              "kernel here runs on a single MI355X; see DESIGN.md for how the path would shard)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import cuflash_attn
+    from cuflash_attn import synth
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    lib = cuflash_attn.load_library()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+
+    # ---------------- config 3: fwd + bwd ----------------
+    B, H, N, D, causal = CFG3["B"], CFG3["H"], CFG3["N"], CFG3["D"], CFG3["causal"]
+    scale = D ** -0.5
+    shape = (B, H, N, D)
+    log("generating config-3 inputs")
+    host = [synth.round_to(synth.normal(s, shape), "bfloat16") for s in (1, 2, 3, 4)]
+    q, k, v, do = (synth.to_torch(x, "bfloat16", dev) for x in host)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, N), device=dev, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    fwd = lib.fn("forward", "bf16")
+    bwd = lib.fn("backward", "bf16")
+    sp = stream.cuda_stream
+
+    def step():
+        st = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H, N,
+                 D, scale, causal, sp)
+        st |= bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                  do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, N, D, scale,
+                  causal, sp)
+        if st != 0:
+            raise RuntimeError(f"library status {st}")
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps")
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+
+    # Per-kernel durations over a second timed region with the event hook on.
+    lib.profile_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    kernels = lib.profile_report()
+    lib.profile_enable(False)
+
+    f_fwd = flops_fwd(B, H, N, D, causal)
+    f_bwd = 2.5 * f_fwd
+    value = (f_fwd + f_bwd) / (ms_per_step * 1e-3) / 1e12
+
+    def avg_ms(label):
+        n, tot = kernels.get(label, (0, 0.0))
+        return tot / n if n else float("nan")
+
+    lbl = {name: f"{name}_bf16_d{D}" for name in
+           ("forward", "backward_delta", "backward_dq", "backward_dkdv")}
+    k_ms = {name: avg_ms(label) for name, label in lbl.items()}
+    # Algorithmic FLOPs per launch: forward = F_fwd. F_bwd counts five N^2 products (S, dP, dV,
+    # dK, dQ); the dkdv kernel performs S, dP, dV, dK (4/5 of F_bwd) and the dq kernel performs
+    # dQ (1/5) plus a recompute of S and dP that the algorithmic count does not include.
+    alg = {
+        "forward": f_fwd,
+        "backward_dq": f_bwd * 1 / 5,
+        "backward_dkdv": f_bwd * 4 / 5,
+    }
+    rooflines = []
+    for name in ("forward", "backward_dq", "backward_dkdv"):
+        ms = k_ms[name]
+        ach = alg[name] / (ms * 1e-3) / 1e12
+        rooflines.append({"kernel": lbl[name], "bound": "mfma", "achieved": round(ach, 2),
+                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(ach / PEAK_BF16_TFLOPS, 4), "avg_ms": round(ms, 4),
+                          "alg_flop_per_launch": alg[name]})
+    dominant = max(rooflines, key=lambda r: r["avg_ms"])
+    roofline = {k2: dominant[k2] for k2 in ("bound", "achieved", "peak", "unit", "frac")}
+    roofline["traffic"] = None
+    roofline["kernel"] = dominant["kernel"]
+    roofline["avg_ms"] = dominant["avg_ms"]
+
+    # ---------------- bounded parity check on the timed data ----------------
+    parity = None
+    if not args.no_parity:
+        import oracle
+
+        log("parity check (2 heads, oracle)")
+        heads = [(0, 0), (B - 1, H - 1)]
+        o_np, l_np = synth.to_numpy(o), synth.to_numpy(lse)
+        dq_np, dk_np, dv_np = (synth.to_numpy(t) for t in (dq, dk, dv))
+        errs = {"O": 0.0, "L": 0.0, "dQ": 0.0, "dK": 0.0, "dV": 0.0}
+        rows = np.arange(0, N, 61, dtype=np.int64)
+        for (b, h) in heads:
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            qh, kh, vh, doh = (x[sl] for x in host)
+            o_ref, l_ref = oracle.forward(qh, kh, vh, scale, causal, nthreads=host_threads())
+            errs["O"] = max(errs["O"], float(np.abs(o_np[sl] - o_ref).max()))
+            errs["L"] = max(errs["L"], float(np.abs(l_np[sl] - l_ref).max()))
+            rq, rk, rv = oracle.backward_rows(qh, kh, vh, doh, scale, causal, rows, rows,
+                                              nthreads=host_threads())
+            errs["dQ"] = max(errs["dQ"], float(np.abs(dq_np[sl][:, :, rows] - rq).max()))
+            errs["dK"] = max(errs["dK"], float(np.abs(dk_np[sl][:, :, rows] - rk).max()))
+            errs["dV"] = max(errs["dV"], float(np.abs(dv_np[sl][:, :, rows] - rv).max()))
+        parity = {"max_abs_err": {k2: round(v2, 6) for k2, v2 in errs.items()}, "tol": 2e-2,
+                  "pass": all(v2 <= 2e-2 for v2 in errs.values()),
+                  "sample": f"heads {heads}, O/L all rows, grads every 61st row"}
+
+    # ---------------- config 4: split-KV decode ----------------
+    decode = None
+    if not args.no_decode:
+        del q, k, v, do, o, dq, dk, dv
+        torch.cuda.empty_cache()
+        Bd, Hd, LKV, Dd = CFG4["B"], CFG4["H"], CFG4["LKV"], CFG4["D"]
+        log("generating config-4 inputs (torch generator on the GPU)")
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        qd = torch.randn((Bd, Hd, 1, Dd), generator=g, device=dev, dtype=torch.float32).half()
+        g.manual_seed(2)
+        kd = torch.randn((Bd, Hd, LKV, Dd), generator=g, device=dev, dtype=torch.float16)
+        g.manual_seed(3)
+        vd = torch.randn((Bd, Hd, LKV, Dd), generator=g, device=dev, dtype=torch.float16)
+        od = torch.empty_like(qd)
+        ld = torch.empty((Bd, Hd, 1), device=dev, dtype=torch.float32)
+        dec = lib.fn("decode", "f16")
+        nbytes = decode_bytes(Bd, Hd, LKV, Dd)
+        results = {}
+        for splits in (16, 32, 64, 0):
+            def run():
+                st = dec(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), od.data_ptr(),
+                         ld.data_ptr(), Bd, Hd, LKV, Dd, Dd ** -0.5, splits, sp)
+                if st != 0:
+                    raise RuntimeError(f"decode status {st}")
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            lib.profile_enable(True)
+            t0.record(stream)
+            for _ in range(args.steps):
+                run()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            rep = lib.profile_report()
+            lib.profile_enable(False)
+            ms = t0.elapsed_time(t1) / args.steps
+            split_ms = rep.get(f"decode_split_f16_d{Dd}", (1, float("nan")))
+            results["auto" if splits == 0 else str(splits)] = {
+                "ms": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "split_kernel_ms": round(split_ms[1] / split_ms[0], 4)}
+        best = max(results.items(), key=lambda kv: kv[1]["GB/s"])
+        split_kernel_gbs = nbytes / (best[1]["split_kernel_ms"] * 1e-3) / 1e9
+        decode = {"metric": "decode HBM GB/s (fp16, B=16 H=32 Lkv=32768 D=128)",
+                  "value": best[1]["GB/s"], "unit": "GB/s", "best_splits": best[0],
+                  "by_splits": results, "alg_bytes": nbytes,
+                  "roofline": {"bound": "hbm", "kernel": f"decode_split_f16_d{Dd}",
+                               "achieved": round(split_kernel_gbs, 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(split_kernel_gbs / PEAK_HBM_GBS, 4),
+                               "traffic": None}}
+        del kd, vd
+
+    # ---------------- CPU baseline (bounded sample) ----------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+
+        threads = host_threads()
+        heads = args.cpu_heads or threads
+        log(f"CPU baseline: naive fp32 fwd+bwd on {heads} heads, {threads} threads")
+        sample = (1, heads, N, D)
+        xs = [synth.normal(s, sample) for s in (1, 2, 3, 4)]
+        c0 = time.perf_counter()
+        oracle.naive_forward_f32(xs[0], xs[1], xs[2], scale, causal, nthreads=threads)
+        oracle.naive_backward_f32(xs[0], xs[1], xs[2], xs[3], scale, causal, nthreads=threads)
+        secs = time.perf_counter() - c0
+        f_sample = flops_fwd(1, heads, N, D, causal) * 3.5
+        cpu = {"value": round(f_sample / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+               "kind": "port", "seconds": round(secs, 2),
+               "sample": f"config-3 shape with B=1 H={heads} (of B*H=32 heads), fwd+bwd, naive "
+                         f"O(N^2) fp32 (reference test_forward.cu:21-118 / test_backward.cu:"
+                         f"21-127 restated in C), one thread per head, same FLOP model"}
+
+    out = {
+        "metric": "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM GB/s at 32k KV",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (SplitMix64/Box-Muller N(0,1), seeds 1-4; decode: torch GPU generator)",
+        "config": {"workload": "cfg3 fwd+bwd: bf16 causal B=2 H=16 N=4096 D=128 (one step = one "
+                               "forward + one backward); cfg4 decode reported under 'decode'",
+                   "batch": B, "heads": H, "seq_len": N, "head_dim": D, "causal": causal},
+        "fwd_ms": round(k_ms["forward"], 4),
+        "bwd_ms": round(k_ms["backward_delta"] + k_ms["backward_dq"] + k_ms["backward_dkdv"], 4),
+        "roofline": roofline,
+        "rooflines": rooflines,
+        "kernel_ms": {kk: round(vv, 4) for kk, vv in k_ms.items()},
+        "decode": decode,
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        out["cpu_baseline"]["gpu_speedup"] = round(value / cpu["value"], 1)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -24,7 +24,7 @@ BUILD_DIR = os.path.join(REPO_ROOT, "build")
 LIB_NAME = "libcuflash_attn.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
 
-SOURCES = ["api.cpp", "forward.hip", "backward.hip", "decode.hip"]
+SOURCES = ["api.cpp", "profile.cpp", "forward.hip", "backward.hip", "decode.hip"]
 
 # Packed-FP32 VALU forms are disabled for all device code (v_pk_{add,mul,fma}_f32).
 COMMON_FLAGS = [

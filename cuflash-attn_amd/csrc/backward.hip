@@ -21,6 +21,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "profile.hpp"
 
 namespace cuflash {
 namespace dev {
@@ -446,8 +447,10 @@ FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O,
     const long long dthreads = rows * LPR;
     const long long dblocks = (dthreads + 255) / 256;
     if (dblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    int tok = profile_kernel<T, D>("backward_delta", stream);
     hipLaunchKernelGGL((dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, o, delta, rows);
+    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
@@ -457,9 +460,11 @@ FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O,
         const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
         const long long blocks = static_cast<long long>(nqb) * BH;
         if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+        tok = profile_kernel<T, D>("backward_dq", stream);
         hipLaunchKernelGGL((dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                            dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
                            reinterpret_cast<E*>(dQ), N, nqb, c, scale, causal ? 1 : 0);
+        profile_end(tok, stream);
         err = from_hip(hipGetLastError());
         if (err != FlashAttentionError::SUCCESS) return err;
     }
@@ -468,10 +473,12 @@ FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O,
         const int nkb = (N + Cfg::BN - 1) / Cfg::BN;
         const long long blocks = static_cast<long long>(nkb) * BH;
         if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+        tok = profile_kernel<T, D>("backward_dkdv", stream);
         hipLaunchKernelGGL((dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                            dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
                            reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), N, nkb, c, scale,
                            causal ? 1 : 0);
+        profile_end(tok, stream);
         err = from_hip(hipGetLastError());
     }
     return err;

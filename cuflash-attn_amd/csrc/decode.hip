@@ -14,6 +14,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "profile.hpp"
 
 namespace cuflash {
 namespace dev {
@@ -273,14 +274,18 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     float* part_acc = static_cast<float*>(ws.get());
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws.get()) + acc_bytes);
 
+    int tok = profile_kernel<T, D>("decode_split", stream);
     hipLaunchKernelGGL((dev::decode_split_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const E*>(Q),
                        reinterpret_cast<const E*>(K), reinterpret_cast<const E*>(V), part_acc,
                        part_ml, kv_len, chunk, nsplit, scale * dev::kLog2e);
+    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
+    tok = profile_kernel<T, D>("decode_combine", stream);
     hipLaunchKernelGGL((dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(BH)), dim3(D),
                        0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L, nsplit);
+    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 

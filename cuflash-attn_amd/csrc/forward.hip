@@ -20,6 +20,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "profile.hpp"
 #include "softmax.hpp"
 
 namespace cuflash {
@@ -352,11 +353,13 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
     const long long blocks = static_cast<long long>(nqb) * BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const int tok = profile_kernel<T, D>("forward", stream);
     hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
                        reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
                        reinterpret_cast<uint16_t*>(O), L, N, nqb, scale * dev::kLog2e,
                        causal ? 1 : 0);
+    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 
@@ -368,9 +371,11 @@ FlashAttentionError run_forward32(const float* Q, const float* K, const float* V
     const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
     const long long blocks = static_cast<long long>(nqb) * BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const int tok = profile_kernel<float, D>("forward", stream);
     hipLaunchKernelGGL((dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, N, nqb,
                        scale * dev::kLog2e, causal ? 1 : 0);
+    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 

@@ -67,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "cuflash_attention_backward_f16", "cuflash_attention_backward_bf16",
     "cuflash_attention_decode_f32", "cuflash_attention_decode_f16",
     "cuflash_attention_decode_bf16", "cuflash_error_string", "cuflash_version",
+    "cuflash_profile_enable", "cuflash_profile_report",
 )
 
 
@@ -87,12 +88,29 @@ class CuFlashLibrary:
         library.cuflash_error_string.restype = ctypes.c_char_p
         library.cuflash_version.argtypes = []
         library.cuflash_version.restype = ctypes.c_char_p
+        library.cuflash_profile_enable.argtypes = [ctypes.c_int]
+        library.cuflash_profile_enable.restype = None
+        library.cuflash_profile_report.argtypes = [ctypes.c_char_p, ctypes.c_int]
+        library.cuflash_profile_report.restype = ctypes.c_int
 
     def error_string(self, code: int) -> str:
         return self.library.cuflash_error_string(int(code)).decode()
 
     def version(self) -> str:
         return self.library.cuflash_version().decode()
+
+    def profile_enable(self, enabled: bool) -> None:
+        self.library.cuflash_profile_enable(1 if enabled else 0)
+
+    def profile_report(self) -> dict:
+        """{label: (launches, total_ms)} for the kernels launched since the last report."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        self.library.cuflash_profile_report(buf, len(buf))
+        out = {}
+        for line in buf.value.decode().splitlines():
+            label, count, ms = line.split("\t")
+            out[label] = (int(count), float(ms))
+        return out
 
     def fn(self, kind: str, suffix: str):
         return getattr(self.library, f"cuflash_attention_{kind}_{suffix}")

@@ -181,6 +181,13 @@ CUFLASH_EXPORT int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const 
 // Library version string (CUFLASH_VERSION); additive.
 CUFLASH_EXPORT const char* cuflash_version(void);
 
+// Measurement hooks (additive; no reference counterpart). While enabled, each kernel launch is
+// bracketed by hipEventRecord on its stream. cuflash_profile_report waits for the recorded
+// events, writes one "label<TAB>launches<TAB>total_ms" line per kernel label into buf (at most
+// buflen bytes, NUL-terminated), clears the records and returns the size the full report needs.
+CUFLASH_EXPORT void cuflash_profile_enable(int enabled);
+CUFLASH_EXPORT int cuflash_profile_report(char* buf, int buflen);
+
 #ifdef __cplusplus
 }
 #endif
