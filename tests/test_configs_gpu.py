@@ -1,0 +1,140 @@
+"""The five BASELINE.json configurations at full size on the GPU.
+
+Parity (north star): FP32 O and L within 1e-4 relative; FP16/BF16 O, L, dQ, dK, dV within
+2e-2 max-abs, against the fp64 oracle on the same rounded inputs. The oracle runs on a subset
+of heads (and of rows for the gradients) so it finishes in seconds; every head is additionally
+checked through size-independent identities:
+  * causal row 0 attends to key 0 only: O_0 = V_0 and L_0 = scale q_0 . k_0;
+  * sum_j dS_ij = 0 for every row, hence sum_j dK_j = scale sum_i Q_i sum_j dS_ij = 0;
+  * rows of P sum to 1, hence sum_j dV_j = sum_i dO_i.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import cuflash_attn
+import oracle
+from conftest import max_abs
+from cuflash_attn import synth
+
+TOL16 = 2e-2
+
+
+def rel(a, b):
+    return max_abs(a, b) / max(float(np.abs(b).max()), 1e-3)
+
+
+def gpu_inputs(shape, dtype, dist, seeds, std=1.0):
+    host = []
+    for s in seeds:
+        x = synth.uniform(s, shape) if dist == "uniform" else synth.normal(s, shape, std)
+        host.append(synth.round_to(x, dtype))
+    return host, [synth.to_torch(x, dtype) for x in host]
+
+
+def check_invariants(q, k, v, o, lse, do, dq, dk, dv, scale, n_tol):
+    """Identities that hold for every head at any size (see module docstring)."""
+    # causal row 0
+    assert max_abs(o[:, :, 0], v[:, :, 0]) <= TOL16
+    s00 = (q[:, :, 0].astype(np.float64) * k[:, :, 0]).sum(-1) * scale
+    assert max_abs(lse[:, :, 0], s00) <= 1e-3
+    if dk is None:
+        return
+    n = q.shape[2]
+    # column sums: bf16 output rounding (<= 2^-9 relative) over n rows bounds the error
+    dk_sum = dk.astype(np.float64).sum(axis=2)
+    assert np.abs(dk_sum).max() <= n_tol * np.sqrt(n), np.abs(dk_sum).max()
+    dv_sum = dv.astype(np.float64).sum(axis=2)
+    do_sum = do.astype(np.float64).sum(axis=2)
+    assert np.abs(dv_sum - do_sum).max() <= n_tol * np.sqrt(n), np.abs(dv_sum - do_sum).max()
+
+
+@pytest.mark.gpu
+def test_config1_fp32_causal(torch_gpu):
+    B, H, N, D = 2, 8, 1024, 64
+    host, (q, k, v) = gpu_inputs((B, H, N, D), "float32", "uniform", (1, 2, 3))
+    o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=D ** -0.5, causal=True)
+    torch_gpu.cuda.synchronize()
+    o_ref, l_ref = oracle.forward(*host, D ** -0.5, True)
+    assert rel(synth.to_numpy(o), o_ref) <= 1e-4
+    assert rel(synth.to_numpy(lse), l_ref) <= 1e-4
+
+
+@pytest.mark.gpu
+def test_config2_fp16_noncausal(torch_gpu):
+    B, H, N, D = 4, 16, 2048, 64
+    host, (q, k, v) = gpu_inputs((B, H, N, D), "float16", "normal", (1, 2, 3))
+    o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=D ** -0.5, causal=False)
+    torch_gpu.cuda.synchronize()
+    o_np, l_np = synth.to_numpy(o), synth.to_numpy(lse)
+    assert np.isfinite(o_np).all() and np.isfinite(l_np).all()
+    for b, h in ((0, 0), (1, 7), (3, 15)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_ref, l_ref = oracle.forward(*(x[sl] for x in host), D ** -0.5, False)
+        assert max_abs(o_np[sl], o_ref) <= TOL16
+        assert max_abs(l_np[sl], l_ref) <= TOL16
+
+
+def _fwd_bwd_config(torch_gpu, B, H, N, D, std, heads, row_step):
+    scale = D ** -0.5
+    host, (q, k, v, do) = gpu_inputs((B, H, N, D), "bfloat16", "normal", (1, 2, 3, 4), std)
+    o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=scale, causal=True)
+    dq, dk, dv = cuflash_attn.flash_attention_backward(q, k, v, o, lse, do, scale=scale,
+                                                       causal=True)
+    torch_gpu.cuda.synchronize()
+    got = [synth.to_numpy(t) for t in (o, lse, dq, dk, dv)]
+    for t in got:
+        assert np.isfinite(t).all()
+    check_invariants(host[0], host[1], host[2], got[0], got[1], host[3], got[2], got[3], got[4],
+                     scale, n_tol=2e-2)
+    rows = np.unique(np.concatenate([np.arange(0, N, row_step), [1, 2, N - 2, N - 1]]))
+    for b, h in heads:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        qh, kh, vh, doh = (x[sl] for x in host)
+        o_ref, l_ref = oracle.forward(qh, kh, vh, scale, True)
+        assert max_abs(got[0][sl], o_ref) <= TOL16
+        assert max_abs(got[1][sl], l_ref) <= TOL16
+        rq, rk, rv = oracle.backward_rows(qh, kh, vh, doh, scale, True, rows, rows)
+        assert max_abs(got[2][sl][:, :, rows], rq) <= TOL16, "dQ"
+        assert max_abs(got[3][sl][:, :, rows], rk) <= TOL16, "dK"
+        assert max_abs(got[4][sl][:, :, rows], rv) <= TOL16, "dV"
+
+
+@pytest.mark.gpu
+def test_config3_bf16_causal_fwd_bwd(torch_gpu):
+    _fwd_bwd_config(torch_gpu, 2, 16, 4096, 128, 1.0, heads=((0, 0), (1, 15)), row_step=37)
+
+
+@pytest.mark.gpu
+def test_config5_bf16_long_context_fwd_bwd(torch_gpu):
+    _fwd_bwd_config(torch_gpu, 1, 32, 16384, 128, 0.5, heads=((0, 31),), row_step=509)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("splits", [16, 32, 64, 0])
+def test_config4_fp16_decode(torch_gpu, splits):
+    torch = torch_gpu
+    B, H, LKV, D = 16, 32, 32768, 128
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    q = torch.randn((B, H, 1, D), generator=g, device=dev, dtype=torch.float32).half()
+    g.manual_seed(2)
+    k = torch.randn((B, H, LKV, D), generator=g, device=dev, dtype=torch.float16)
+    g.manual_seed(3)
+    v = torch.randn((B, H, LKV, D), generator=g, device=dev, dtype=torch.float16)
+    o, lse = cuflash_attn.flash_attention_decode(q, k, v, scale=D ** -0.5, num_splits=splits)
+    torch.cuda.synchronize()
+    o_np, l_np = synth.to_numpy(o), synth.to_numpy(lse)
+    assert np.isfinite(o_np).all() and np.isfinite(l_np).all()
+    for b, h in ((0, 0), (7, 19), (15, 31)):
+        qh = synth.to_numpy(q[b:b + 1, h:h + 1])
+        kh = synth.to_numpy(k[b:b + 1, h:h + 1])
+        vh = synth.to_numpy(v[b:b + 1, h:h + 1])
+        o_ref, l_ref = oracle.forward(qh, kh, vh, D ** -0.5, False)
+        assert max_abs(o_np[b:b + 1, h:h + 1], o_ref) <= TOL16
+        assert max_abs(l_np[b:b + 1, h:h + 1], l_ref) <= TOL16
+    del k, v
+    torch.cuda.empty_cache()
