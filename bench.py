@@ -47,6 +47,55 @@ def decode_bytes(B, H, LKV, D, elem=2):
     return B * H * D * (2 * LKV + 2) * elem + B * H * 4
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic_pmc.md")
+
+
+def committed_traffic(kernel_label):
+    """HBM bytes per launch of `kernel_label` from the committed rocprofv3 PMC summary (lines
+    `traffic: <label> <bytes>`), or None when that kernel has no committed measurement."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel_label:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_workload(kind):
+    """Short fixed workloads for rocprofv3 --pmc passes (no timing, no output line):
+    cfg3 = 2 x (forward + backward) of config 3; decode = 2 x config-4 decode (auto splits);
+    copy = one device-to-device copy of 1 GiB, the calibration kernel for FETCH_SIZE and
+    WRITE_SIZE."""
+    import torch
+
+    import cuflash_attn
+
+    dev = torch.device("cuda:0")
+    if kind == "copy":
+        a = torch.ones(1 << 28, device=dev, dtype=torch.float32)
+        b = torch.empty_like(a)
+        b.copy_(a)
+    elif kind == "cfg3":
+        c = CFG3
+        xs = [torch.randn((c["B"], c["H"], c["N"], c["D"]), device=dev).to(torch.bfloat16)
+              for _ in range(4)]
+        for _ in range(2):
+            o, lse = cuflash_attn.flash_attention_forward(*xs[:3], causal=True)
+            cuflash_attn.flash_attention_backward(*xs[:3], o, lse, xs[3], causal=True)
+    elif kind == "decode":
+        c = CFG4
+        q = torch.randn((c["B"], c["H"], 1, c["D"]), device=dev).half()
+        k = torch.randn((c["B"], c["H"], c["LKV"], c["D"]), device=dev, dtype=torch.float16)
+        v = torch.randn_like(k)
+        for _ in range(2):
+            cuflash_attn.flash_attention_decode(q, k, v, num_splits=0)
+    torch.cuda.synchronize()
+    return 0
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,6 +104,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--pmc-workload", choices=("cfg3", "decode", "copy"), default=None,
+                    help="run only a short fixed workload for rocprofv3 --pmc passes")
     ap.add_argument("--cpu-heads", type=int, default=0,
                     help="heads in the CPU-baseline sample (default: one per host thread, <= 16)")
     return ap.parse_args()
@@ -79,6 +130,9 @@ def main():
               "kernel here runs on a single MI355X; see DESIGN.md for how the path would shard)",
               file=sys.stderr)
         return 2
+
+    if args.pmc_workload:
+        return pmc_workload(args.pmc_workload)
 
     import numpy as np
     import torch
@@ -144,32 +198,28 @@ def main():
     f_bwd = 2.5 * f_fwd
     value = (f_fwd + f_bwd) / (ms_per_step * 1e-3) / 1e12
 
-    def avg_ms(label):
-        n, tot = kernels.get(label, (0, 0.0))
-        return tot / n if n else float("nan")
-
-    lbl = {name: f"{name}_bf16_d{D}" for name in
-           ("forward", "backward_delta", "backward_dq", "backward_dkdv")}
-    k_ms = {name: avg_ms(label) for name, label in lbl.items()}
-    # Algorithmic FLOPs per launch: forward = F_fwd. F_bwd counts five N^2 products (S, dP, dV,
-    # dK, dQ); the dkdv kernel performs S, dP, dV, dK (4/5 of F_bwd) and the dq kernel performs
-    # dQ (1/5) plus a recompute of S and dP that the algorithmic count does not include.
-    alg = {
-        "forward": f_fwd,
-        "backward_dq": f_bwd * 1 / 5,
-        "backward_dkdv": f_bwd * 4 / 5,
-    }
+    # Algorithmic FLOPs per launch: forward = F_fwd; F_bwd counts five N^2 products (S, dP, dV,
+    # dK, dQ). The fused backward performs all five once (F_bwd). The deterministic two-pass
+    # backward splits them: dkdv performs S, dP, dV, dK (4/5 of F_bwd), dq performs dQ (1/5)
+    # plus a recompute of S and dP that the algorithmic count does not include.
+    alg = {"forward": f_fwd, "backward_fused": f_bwd, "backward_dq": f_bwd / 5,
+           "backward_dkdv": f_bwd * 4 / 5}
+    suffix = f"_bf16_d{D}"
+    k_ms = {label[:-len(suffix)]: tot / n for label, (n, tot) in kernels.items()
+            if label.endswith(suffix) and n}
     rooflines = []
-    for name in ("forward", "backward_dq", "backward_dkdv"):
+    for name, flop in alg.items():
+        if name not in k_ms:
+            continue
         ms = k_ms[name]
-        ach = alg[name] / (ms * 1e-3) / 1e12
-        rooflines.append({"kernel": lbl[name], "bound": "mfma", "achieved": round(ach, 2),
+        ach = flop / (ms * 1e-3) / 1e12
+        rooflines.append({"kernel": name + suffix, "bound": "mfma", "achieved": round(ach, 2),
                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                           "frac": round(ach / PEAK_BF16_TFLOPS, 4), "avg_ms": round(ms, 4),
-                          "alg_flop_per_launch": alg[name]})
+                          "alg_flop_per_launch": flop})
     dominant = max(rooflines, key=lambda r: r["avg_ms"])
     roofline = {k2: dominant[k2] for k2 in ("bound", "achieved", "peak", "unit", "frac")}
-    roofline["traffic"] = None
+    roofline["traffic"] = committed_traffic(dominant["kernel"])
     roofline["kernel"] = dominant["kernel"]
     roofline["avg_ms"] = dominant["avg_ms"]
 
@@ -248,7 +298,7 @@ def main():
                   "roofline": {"bound": "hbm", "kernel": f"decode_split_f16_d{Dd}",
                                "achieved": round(split_kernel_gbs, 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(split_kernel_gbs / PEAK_HBM_GBS, 4),
-                               "traffic": None}}
+                               "traffic": committed_traffic(f"decode_split_f16_d{Dd}")}}
         del kd, vd
 
     # ---------------- CPU baseline (bounded sample) ----------------
@@ -289,7 +339,7 @@ def main():
                                "forward + one backward); cfg4 decode reported under 'decode'",
                    "batch": B, "heads": H, "seq_len": N, "head_dim": D, "causal": causal},
         "fwd_ms": round(k_ms["forward"], 4),
-        "bwd_ms": round(k_ms["backward_delta"] + k_ms["backward_dq"] + k_ms["backward_dkdv"], 4),
+        "bwd_ms": round(sum(v2 for k2, v2 in k_ms.items() if k2.startswith("backward")), 4),
         "roofline": roofline,
         "rooflines": rooflines,
         "kernel_ms": {kk: round(vv, 4) for kk, vv in k_ms.items()},

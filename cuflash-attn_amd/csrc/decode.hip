@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256)
     const int split = blockIdx.x % nsplit;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int grp = lane / LPR;   // row slot inside a wave load
     const int part = lane % LPR;  // which 16-byte chunk of the row
 

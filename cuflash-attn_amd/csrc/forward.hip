@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(256, 2)
     const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
@@ -129,7 +129,8 @@ __global__ void __launch_bounds__(256, 2)
         if (kb + 1 < nkb) fetch(kb + 1);
 
         const int key0 = kb * Cfg::BN;
-        if (causal && key0 > q0 + 31) continue;  // whole block lies in this wave's future
+        // A wave whose rows all precede the block still runs it (every P is 0 there): a branch
+        // around the MFMAs would force copies of the O accumulators on every iteration.
 
         // S^T = K Q^T for the two 32-key tiles of the block.
         f32x16 s[2];
@@ -218,7 +219,7 @@ __global__ void __launch_bounds__(256, 2)
     const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
@@ -286,7 +287,6 @@ __global__ void __launch_bounds__(256, 2)
         if (kb + 1 < nkb) fetch(kb + 1);
 
         const int key0 = kb * Cfg::BN;
-        if (causal && key0 > q0 + 31) continue;
 
         f32x16 s[1];
         s[0] = f32x16{};

@@ -67,7 +67,7 @@ def test_forward_parity(torch_gpu, dtype, d, causal, n):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("n", [1, 33, 130])
+@pytest.mark.parametrize("n", [1, 33, 130, 300])
 def test_backward_parity(torch_gpu, dtype, d, causal, n):
     shape = (1, 2, n, d)
     q, k, v, do = make_inputs(shape, dtype)
