@@ -31,6 +31,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kFltMin = 1.17549435e-38f;  // smallest normal float
 
 // ---------------------------------------------------------------------------------------------
 // Element traits. 16-bit types are moved around as raw uint16_t bit patterns; conversions use
@@ -220,11 +221,48 @@ struct Mma<float> {
     }
 };
 
+// Transpose-read operand from two explicit LDS byte addresses (the rows k0 + kslot(h, 0..3) and
+// k0 + 8 + kslot(h, 0..3) of the same layout as read_tr_frag).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag tr_frag_at(const unsigned char* p0,
+                                                             const unsigned char* p1) {
+    const i16x4 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(p0));
+    const i16x4 hi = lds_read_tr16(reinterpret_cast<const uint16_t*>(p1));
+    u32x4 v;
+    v[0] = __builtin_bit_cast(u32x2, lo)[0];
+    v[1] = __builtin_bit_cast(u32x2, lo)[1];
+    v[2] = __builtin_bit_cast(u32x2, hi)[0];
+    v[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_frag<T>(v);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Global -> LDS direct loads (gfx950 global_load_lds_dwordx4): lane i of the wave writes the 16
+// bytes at its own global address to lds_base + 16 * i (verified on gfx950). lds_base must be
+// wave-uniform; the load is tracked by vmcnt like any other global load.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16(const void* src, unsigned char* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_base), 16,
+                                     0, 0);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float xor_shuffle(float v, int mask) {
     return __shfl_xor(v, mask, 64);
+}
+
+// max / sum of v over the lane pair (l, l ^ 32), with gfx950's v_permlane32_swap (VALU, no LDS).
+__device__ __forceinline__ float pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -242,6 +280,23 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     if (nblocks % kNumXcd != 0) return bid;
     const int per_xcd = nblocks / kNumXcd;
     return (bid % kNumXcd) * per_xcd + bid / kNumXcd;
+}
+
+// Workgroup id -> (head, rank) for grids of BH heads x nranks blocks whose blocks of one head
+// share K/V. When BH is a multiple of 8 every XCD gets BH / 8 whole heads (their K/V stay in its
+// L2) and, inside an XCD, blocks are dispatched rank-major (rank 0 of each of its heads, then
+// rank 1, ...); otherwise ranks are dispatched round-robin over all heads. Kernels map rank 0 to
+// their longest block, so long blocks start first in either case.
+__device__ __forceinline__ void head_rank_order(int bid, int BH, int& bh, int& rank) {
+    if (BH % kNumXcd == 0) {
+        const int hpx = BH / kNumXcd;
+        const int k = bid / kNumXcd;
+        rank = k / hpx;
+        bh = (bid % kNumXcd) * hpx + k % hpx;
+    } else {
+        rank = bid / BH;
+        bh = bid % BH;
+    }
 }
 
 }  // namespace dev

@@ -191,6 +191,245 @@ __global__ void __launch_bounds__(256, 2)
 }
 
 // ------------------------------------------------------------------------------------------
+// fp16 / bf16 kernel for head_dim 128 (the headline shape), software-pipelined
+// ------------------------------------------------------------------------------------------
+// Same decomposition and numerics as fwd16_kernel (128 query rows per workgroup, 32 per wave,
+// S^T = K Q^T with Q^T in registers, O^T += V^T P^T), restructured for gfx950:
+//  * K and V blocks of 64 keys go global -> LDS with global_load_lds_dwordx4 (no staging
+//    registers, no VALU or ds_write for the copy) into double buffers, so one barrier per block
+//    suffices and the next blocks load while the current one is consumed;
+//  * LDS layout of a 64 x 128 tile: 16 groups of 4 rows, 1088 bytes each (1 KB + 64 bytes of
+//    padding); inside a group the 16-byte chunk c of row r sits at (4 c + r % 4) * 16. One load
+//    instruction fills one group (lane i: row r0 + i % 4, chunk i / 4, i.e. 1 KB of contiguous
+//    global memory), and both consumers read conflict-free with immediate offsets: the K row
+//    reads of S^T (16 rows, one chunk: 4 groups x 4 rows -> 16 distinct 16-byte bank slots) and
+//    the V transpose reads of P V (4 rows x 4 chunks of one group: 256 contiguous bytes);
+//  * the scores of block j+1 are formed by MFMA while the softmax of block j runs on the VALU
+//    (two score register sets), and P V of block j follows;
+//  * the lane-pair row max / sum use v_permlane32_swap instead of an LDS permute.
+template <typename T>
+__global__ void __launch_bounds__(256, 2)
+    fwd16_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                      const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
+                      float* __restrict__ L, int N, int nqb, float c, int causal) {
+    constexpr int D = 128;
+    constexpr int BM = 128;
+    constexpr int BN = 64;
+    constexpr int GRP = 1088;              // bytes per 4-row group
+    constexpr int TILE = (BN / 4) * GRP;   // bytes per 64-row tile
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
+
+    int bh, rank;
+    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * N * D;
+    const uint16_t* Kh = K + head;
+    const uint16_t* Vh = V + head;
+    const int q0 = qb * BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;              // query row owned by this lane
+
+    frag qf[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < N) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    const int kv_end = causal ? min(N, (qb + 1) * BM) : N;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    // Loads of one 64-row tile: wave w fills groups w, w + 4, w + 8, w + 12. Rows past N are
+    // clamped to row N - 1 (finite values; their scores are masked).
+    const int ld_row = lane & 3;
+    const int ld_col = (lane >> 2) * 8;
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int grp = wave + 4 * i;
+            const int row = min(key0 + 4 * grp + ld_row, N - 1);
+            lds_dma16(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
+        }
+    };
+    // Per-lane byte offsets of the operand reads (see the layout above).
+    const int k_off = (l32 >> 2) * GRP + g2 * 64 + (l32 & 3) * 16;
+    const int kq = lane & 15;
+    const int v_off = g2 * GRP + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 +
+                      (kq & 1) * 8;
+
+    auto scores = [&](const unsigned char* kt, f32x16 (&s)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks)
+                s[t] = Elem<T>::mma(as_frag<T>(ld16(kt + k_off + 8 * t * GRP + ks * 128)), qf[ks],
+                                    s[t]);
+        }
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;  // running max of s * cs (log2 units)
+    float l = 0.0f;       // this lane's share of the running row sum
+    // Exponent scale, kept positive so that a masked score (-inf) always maps to p = 0, also
+    // for scale = 0 (where FLT_MIN leaves every p at 1 and L at log(count), as with 0).
+    const float cs = fmaxf(c, kFltMin);
+
+    // Keys past N and, with a causal mask, keys after this lane's row get s = -inf.
+    auto mask_scores = [&](f32x16 (&s)[2], int key0) {
+        const int lim = min(N, causal ? q + 1 : N) - key0 - 4 * g2;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 32 * t + 8 * (r >> 2) + (r & 3);
+                s[t][r] = off < lim ? s[t][r] : -INFINITY;
+            }
+        }
+    };
+
+    // Row max of one block and the online-softmax update of (m, l). Returns whether some lane
+    // of the wave must rescale its O by alpha. The lazy rescale is decided per lane with
+    // selects: m only moves when the block max exceeds it by more than kLazyRescale, and O and
+    // l of that lane are scaled by the same alpha, so the result is exact either way.
+    auto update_max = [&](const f32x16 (&s)[2], float& alpha) -> bool {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+        }
+        const float m_new = fmaxf(m, pair_max(mx) * cs);
+        const bool grow = m_new > m + kLazyRescale;
+        const float a_raw = fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new);
+        alpha = grow ? a_raw : 1.0f;
+        m = grow ? m_new : m;
+        l *= alpha;
+        return __ballot(grow) != 0;
+    };
+
+    // One pipelined step, free of branches so that the scheduler can interleave it: the MFMAs
+    // of the next block's scores (from tile kt) run while the current scores become P (exp,
+    // row sum, rounding to T), then O^T += V^T P^T from V tile vt.
+    auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
+                    const unsigned char* vt) {
+        scores(kt, s_next);
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = fast_exp2(fmaf(s[t][r], cs, -m_use));
+                s[t][r] = e;
+                sum += e;
+            }
+        }
+        l += sum;
+        frag p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = j >> 1;
+            const int h = j & 1;
+            p[j] = pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2], s[t][8 * h + 3],
+                                s[t][8 * h + 4], s[t][8 * h + 5], s[t][8 * h + 6],
+                                s[t][8 * h + 7]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const unsigned char* a0 = vt + v_off + 4 * j * GRP + dt * 256;
+                o[dt] = Elem<T>::mma(tr_frag_at<T>(a0, a0 + 2 * GRP), p[j], o[dt]);
+            }
+        }
+        // Interleave the score MFMAs with the softmax VALU work: a few K reads ahead, then per
+        // MFMA one more K read and about seven VALU ops; the P V MFMAs and their V reads follow.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        }
+    };
+
+    // Blocks that need masking: keys past N, and with a causal mask the blocks that reach past
+    // this wave's first row.
+    auto needs_mask = [&](int key0) { return key0 + BN > N || (causal && key0 + BN - 1 > q0); };
+
+    // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
+    // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
+    // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
+    // buffers. Each iteration also forms the scores of block j+1 (for the last block they are
+    // formed from a stale buffer and discarded, which keeps the step free of branches). The
+    // loop is unrolled by two so that every buffer is a distinct LDS object.
+    load_tile(Kh, 0, Kb0);
+    load_tile(Vh, 0, Vb0);
+    if (nkb > 1) load_tile(Kh, BN, Kb1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    f32x16 sa[2], sb[2];
+    float alpha;
+    scores(Kb0, sa);
+    for (int j = 0; j < nkb; j += 2) {
+        // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 2 < nkb) load_tile(Kh, (j + 2) * BN, Kb0);
+        if (j + 1 < nkb) load_tile(Vh, (j + 1) * BN, Vb1);
+        if (needs_mask(j * BN)) mask_scores(sa, j * BN);
+        if (update_max(sa, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+        step(sa, Kb1, sb, Vb0);
+        if (j + 1 >= nkb) break;
+        // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 3 < nkb) load_tile(Kh, (j + 3) * BN, Kb1);
+        if (j + 2 < nkb) load_tile(Vh, (j + 2) * BN, Vb0);
+        if (needs_mask((j + 1) * BN)) mask_scores(sb, (j + 1) * BN);
+        if (update_max(sb, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+        step(sb, Kb0, sa, Vb1);
+    }
+
+    // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
+    l = pair_sum(l);
+    if (q < N) {
+        const float inv = 1.0f / l;
+        uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                u32x2 w;
+                w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
+                w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
+                st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // fp32 kernel
 // ------------------------------------------------------------------------------------------
 template <int D>
@@ -354,11 +593,19 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     const long long blocks = static_cast<long long>(nqb) * BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int tok = profile_kernel<T, D>("forward", stream);
-    hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
-                       reinterpret_cast<const uint16_t*>(K), reinterpret_cast<const uint16_t*>(V),
-                       reinterpret_cast<uint16_t*>(O), L, N, nqb, scale * dev::kLog2e,
-                       causal ? 1 : 0);
+    if constexpr (D == 128) {
+        hipLaunchKernelGGL((dev::fwd16_d128_kernel<T>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+                           reinterpret_cast<const uint16_t*>(K),
+                           reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
+                           L, N, nqb, scale * dev::kLog2e, causal ? 1 : 0);
+    } else {
+        hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+                           reinterpret_cast<const uint16_t*>(K),
+                           reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
+                           L, N, nqb, scale * dev::kLog2e, causal ? 1 : 0);
+    }
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
