@@ -18,12 +18,15 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
+// For fp16/bf16 at head_dim 128 the same three steps run as delta_ld_kernel, dq_d128_kernel
+// and dkdv_d128_kernel (section 4). Every path is deterministic: no atomics, and each output
+// element is written by exactly one lane.
 
 #include "common.hpp"
 #include "launch.hpp"
 #include "profile.hpp"
 
-#include <cstdlib>
+#include <type_traits>
 
 namespace cuflash {
 namespace dev {
@@ -95,13 +98,11 @@ __device__ __forceinline__ float dot16(u32x4 a, u32x4 b) {
     return s;
 }
 
-// When dq_acc is non-null the kernel also clears the fp32 dQ accumulator of the fused backward
-// (the same rows, VEC floats per lane), which saves a separate fill pass over it.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     delta_kernel(const typename Mma<T>::elem* __restrict__ dO,
                  const typename Mma<T>::elem* __restrict__ O, float* __restrict__ Dst,
-                 float* __restrict__ dq_acc, long long rows) {
+                 long long rows) {
     using E = typename Mma<T>::elem;
     constexpr int VEC = 16 / static_cast<int>(sizeof(E));
     constexpr int LPR = D / VEC;  // lanes per row
@@ -112,10 +113,6 @@ __global__ void __launch_bounds__(256)
     if (row < rows) {
         const size_t off = static_cast<size_t>(row) * D + part * VEC;
         s = dot16<T>(ld16(dO + off), ld16(O + off));
-        if (dq_acc) {
-#pragma unroll
-            for (int i = 0; i < VEC; i += 4) st16(dq_acc + off + i, u32x4{0u, 0u, 0u, 0u});
-        }
     }
 #pragma unroll
     for (int w = LPR / 2; w > 0; w >>= 1) s += xor_shuffle(s, w);
@@ -430,74 +427,90 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// 4. Fused dK, dV, dQ (fp16 / bf16): one pass, five products per tile
+// 4. Backward for head_dim 128 (fp16 / bf16)
 // ------------------------------------------------------------------------------------------
-// KV-stationary like dkdv_kernel (each wave owns 32 keys, the workgroup 128), but every query
-// block also yields its dQ contribution: the waves write dS^T (rounded to T) to LDS, and after
-// one barrier wave w forms the 32x32 tile dQ[q0:q0+32, 32*(w % NDT) : +32] over the workgroup's
-// keys (A = dS via transpose reads of dS^T, B = K via transpose reads of the LDS copy of K) and
-// adds it to an fp32 accumulator in HBM with global_atomic_add_f32. No score is computed twice
-// (S, dP, dV, dK, dQ), against seven products for dq_kernel + dkdv_kernel.
-// The query blocks are double-buffered in LDS (Q and dO in a row-read layout and a
-// transpose-read layout, L and D), and so is dS^T, so one barrier per block suffices:
-//   compute block i from buffer b; write dS^T[b]; stage block i+1 into buffer b^1 (fetched into
-//   registers one block earlier); fetch block i+2; barrier; dQ of block i from dS^T[b].
-// The atomics of block i are issued during block i+1, after its first products, so their wait
-// on the dQ products overlaps with other work.
-template <int D>
-struct FusedCfg {
-    static constexpr int kThreads = 256;
-    static constexpr int BN = 128;  // keys per workgroup (32 per wave)
-    static constexpr int BM = 32;   // query rows per block
-    static constexpr int RP = D + 8;                              // row-read pitch (Q, dO)
-    static constexpr int CP = ((2 * D) % 128 == 64) ? D : D + 32;  // transpose-read pitch
-    static constexpr int SP = 32;   // dS^T pitch: 4 rows of 64 bytes cover the 64 banks
-    static constexpr int NDT = D / 32;      // 32-column tiles of dQ
-    static constexpr int KSPLIT = 4 / NDT;  // waves per dQ tile, each over BN / KSPLIT keys
-    static constexpr int KSTEPS = BN / KSPLIT / 16;  // 16-key MFMA steps per wave for dQ
-};
+// Row statistics for the D = 128 kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
+// (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
+// without any masking.
+template <typename T>
+__global__ void __launch_bounds__(256)
+    delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
+                    const float* __restrict__ L, float2* __restrict__ LD, int N, int Npad,
+                    long long rows_pad) {
+    constexpr int D = 128;
+    constexpr int LPR = D / 8;  // lanes per row
+    const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    const long long prow = t / LPR;  // padded row index
+    const int part = static_cast<int>(t % LPR);
+    const long long bh = prow / Npad;
+    const int r = static_cast<int>(prow % Npad);
+    const bool real = prow < rows_pad && r < N;
+    float s = 0.0f;
+    if (real) {
+        const size_t off = static_cast<size_t>(bh * N + r) * D + part * 8;
+        s = dot16<T>(ld16(dO + off), ld16(O + off));
+    }
+#pragma unroll
+    for (int w = LPR / 2; w > 0; w >>= 1) s += xor_shuffle(s, w);
+    if (prow < rows_pad && part == 0)
+        LD[prow] = real ? make_float2(L[bh * N + r] * kLog2e, s) : make_float2(INFINITY, 0.0f);
+}
 
-template <typename T, int D>
-__global__ void __launch_bounds__(256, 1)
-    bwd_fused_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                     const uint16_t* __restrict__ V, const float* __restrict__ L,
-                     const uint16_t* __restrict__ dO, const float* __restrict__ Dl,
-                     float* __restrict__ dq_acc, uint16_t* __restrict__ dK,
-                     uint16_t* __restrict__ dV, int N, int nkb, float c, float scale,
+// ------------------------------------------------------------------------------------------
+// dkdv_d128_kernel and dq_d128_kernel restate dkdv_kernel and dq_kernel (same products, same
+// rounding of P and dS to T) with a gfx950 data path: tiles go global -> LDS by direct loads
+// (global_load_lds_dwordx4, issued from inline assembly so that buffers can rotate at run time)
+// into the padded 4-row-group layout of fwd16_d128_kernel, whose single copy of a tile serves
+// both the row reads of S = Q K^T / dP = dO V^T and the transpose reads of dV^T += dO^T P /
+// dK^T += Q^T dS / dQ^T += K^T dS^T without bank conflicts; blocks are double-buffered with one
+// barrier per block; (L log2 e, D) rows come padded from delta_ld_kernel; and the register
+// budget allows two workgroups per CU, so the two waves of each SIMD hide each other's
+// latencies.
+constexpr int kGrp128 = 1088;  // bytes per 4-row group of a 128-wide 16-bit tile
+
+// Per-lane byte offsets into the 4-row-group layout (see fwd16_d128_kernel).
+__device__ __forceinline__ int grp_row_off() {  // A operand: 32 rows x 16 k (row reads)
+    const int lane = threadIdx.x & 63;
+    return ((lane & 31) >> 2) * kGrp128 + (lane >> 5) * 64 + (lane & 3) * 16;
+}
+__device__ __forceinline__ int grp_tr_sub() {  // transpose reads, without the row-half term
+    const int lane = threadIdx.x & 63;
+    const int kq = lane & 15;
+    return (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 + (kq & 1) * 8;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256, 2)
+    dkdv_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
+                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
+                     uint16_t* __restrict__ dV, int N, int Npad, int nkb, float c, float scale,
                      int causal) {
+    constexpr int D = 128;
+    constexpr int BN = 128;  // keys per workgroup (32 per wave)
+    constexpr int BM = 32;   // query rows per block
+    constexpr int GRP = kGrp128;
+    constexpr int QT = (BM / 4) * GRP;
+    constexpr int SET = 2 * QT + BM * 8;  // Q tile, dO tile, 32 x (L, D)
     using frag = typename Elem<T>::frag;
-    using Cfg = FusedCfg<D>;
-    constexpr int BM = Cfg::BM;
-    constexpr int RP = Cfg::RP;
-    constexpr int CP = Cfg::CP;
-    constexpr int SP = Cfg::SP;
-    __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BM * RP];
-    __shared__ __attribute__((aligned(16))) uint16_t Qc[2][BM * CP];
-    __shared__ __attribute__((aligned(16))) uint16_t Os[2][BM * RP];
-    __shared__ __attribute__((aligned(16))) uint16_t Oc[2][BM * CP];
-    __shared__ __attribute__((aligned(16))) uint16_t St[2][Cfg::BN * SP];
-    __shared__ __attribute__((aligned(16))) uint16_t Kc[Cfg::BN * CP];
-    __shared__ __attribute__((aligned(16))) float Ls[2][BM];
-    __shared__ __attribute__((aligned(16))) float Ds[2][BM];
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * SET];
 
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = lid / nkb;
-    const int kb = lid % nkb;  // ascending: with a causal mask the first blocks carry the most work
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    int bh, kb;
+    head_rank_order(blockIdx.x, gridDim.x / nkb, bh, kb);  // kb = 0 (most work) first
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
     const size_t head = static_cast<size_t>(bh) * N * D;
-    const float* Lh = L + static_cast<size_t>(bh) * N;
-    const float* Dh = Dl + static_cast<size_t>(bh) * N;
-    const int kwg = kb * Cfg::BN;             // first key of the workgroup
-    const int k0 = kwg + wave * 32;           // first key of this wave
-    const int key = k0 + l32;                 // key row owned by this lane
+    const uint16_t* Qh = Q + head;
+    const uint16_t* Oh = dO + head;
+    const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
+    const int kwg = kb * BN;
+    const int k0 = kwg + wave * 32;
+    const int key = k0 + l32;
     const bool key_ok = key < N;
 
-    // K and V of this lane's key as B operands (k = d), and K of the whole workgroup in LDS.
     frag kf[D / 16];
     frag vf[D / 16];
 #pragma unroll
@@ -510,11 +523,23 @@ __global__ void __launch_bounds__(256, 1)
         kf[ks] = as_frag<T>(kv);
         vf[ks] = as_frag<T>(vv);
     }
-    {
-        TileCopy<uint16_t, Cfg::BN, D, Cfg::kThreads> kcp;
-        kcp.fetch(K + head + static_cast<size_t>(kwg) * D, N - kwg, tid);
-        kcp.stage(Kc, CP, tid);
-    }
+
+    const int ld_row = lane & 3;
+    const int ld_col = (lane >> 2) * 8;
+    auto load_block = [&](int qb, int b) {
+        const int r0 = qb * BM;
+        unsigned char* set = smem + b * SET;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int grp = wave + 4 * i;
+            const int row = min(r0 + 4 * grp + ld_row, N - 1);
+            lds_dma16_async(Qh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
+            lds_dma16_async(Oh + static_cast<size_t>(row) * D + ld_col, set + QT + grp * GRP);
+        }
+        if (wave == 3) lds_dma4_async(LDh + 2 * r0 + lane, set + 2 * QT);
+    };
+    const int row_off = grp_row_off();
+    const int tr_off = g2 * GRP + grp_tr_sub();
 
     f32x16 dk[D / 32];
     f32x16 dv[D / 32];
@@ -523,143 +548,69 @@ __global__ void __launch_bounds__(256, 1)
         dk[dt] = f32x16{};
         dv[dt] = f32x16{};
     }
-
-    const int nqb = (N + BM - 1) / BM;
+    const float cs = fmaxf(c, kFltMin);
+    const int nqb = Npad / BM;
     const int qb_begin = causal ? kwg / BM : 0;
-    TileCopy<uint16_t, BM, D, Cfg::kThreads> qcp, ocp;
-    float lreg = 0.0f;
-    auto fetch = [&](int qb) {
-        const int r0 = qb * BM;
-        qcp.fetch(Q + head + static_cast<size_t>(r0) * D, N - r0, tid);
-        ocp.fetch(dO + head + static_cast<size_t>(r0) * D, N - r0, tid);
-        if (tid < 2 * BM) {
-            const int r = r0 + (tid % BM);
-            if (tid < BM)
-                lreg = r < N ? Lh[r] * kLog2e : INFINITY;  // rows past N: P = 0
-            else
-                lreg = r < N ? Dh[r] : 0.0f;
-        }
-    };
-    auto stage = [&](int b) {
-        qcp.stage(Qs[b], RP, tid);
-        qcp.stage(Qc[b], CP, tid);
-        ocp.stage(Os[b], RP, tid);
-        ocp.stage(Oc[b], CP, tid);
-        if (tid < BM)
-            Ls[b][tid] = lreg;
-        else if (tid < 2 * BM)
-            Ds[b][tid - BM] = lreg;
-    };
 
-    const int tr_c = tr_lane_offset(CP);
-    const int tr_s = tr_lane_offset(SP);
-    const int dtile = wave % Cfg::NDT;           // dQ column tile of this wave
-    const int jbeg = (wave / Cfg::NDT) * Cfg::KSTEPS;  // first 16-key step of its key range
-    float* dq_head = dq_acc + head;
-
-    f32x16 dq_prev = f32x16{};
-    int q0_prev = -1;
-    auto flush_dq = [&]() {
-        if (q0_prev < 0) return;
-        float* base = dq_head + 32 * dtile + l32;
-        if (q0_prev + BM <= N) {  // wave-uniform: every row of the block exists
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int q = q0_prev + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                unsafeAtomicAdd(base + static_cast<size_t>(q) * D, dq_prev[r]);
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int q = q0_prev + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (q < N) unsafeAtomicAdd(base + static_cast<size_t>(q) * D, dq_prev[r]);
-            }
-        }
-    };
-
-    if (qb_begin < nqb) {
-        fetch(qb_begin);
-        stage(0);
-        if (qb_begin + 1 < nqb) fetch(qb_begin + 1);
-    }
-    __syncthreads();
-
-    for (int qb = qb_begin; qb < nqb; ++qb) {
-        const int b = (qb - qb_begin) & 1;
+    load_block(qb_begin, 0);
+    int b = 0;
+    for (int qb = qb_begin; qb < nqb; ++qb, b ^= 1) {
         const int q0 = qb * BM;
-        // Every wave runs every block, also where all of its keys are masked (P = 0): a branch
-        // around the MFMAs would make the compiler copy the dK/dV accumulators between AGPRs
-        // and VGPRs on every iteration.
+        __builtin_amdgcn_s_waitcnt(0);  // block qb is in LDS
+        __syncthreads();                // ... for every wave; block qb - 1 is no longer read
+        if (qb + 1 < nqb) load_block(qb + 1, b ^ 1);
+        const unsigned char* qt = smem + b * SET;
+        const unsigned char* ot = qt + QT;
+        const float2* ldv = reinterpret_cast<const float2*>(qt + 2 * QT);
+
+        // S = Q K^T and dP = dO V^T: rows = queries, lane = key.
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
-        // S = Q K^T and dP = dO V^T: rows = queries, column = this lane's key.
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-            s = Elem<T>::mma(as_frag<T>(ld16(&Qs[b][l32 * RP + 16 * ks + 8 * g2])), kf[ks], s);
-            dp = Elem<T>::mma(as_frag<T>(ld16(&Os[b][l32 * RP + 16 * ks + 8 * g2])), vf[ks], dp);
+            s = Elem<T>::mma(as_frag<T>(ld16(qt + row_off + ks * 128)), kf[ks], s);
+            dp = Elem<T>::mma(as_frag<T>(ld16(ot + row_off + ks * 128)), vf[ks], dp);
         }
-        flush_dq();  // atomics of the previous block, behind this block's first products
-
-        {
-            const bool masked = (causal && k0 + 31 > q0) || (k0 + 31 >= N);
+        if ((causal && k0 + 31 > q0) || k0 + 31 >= N) {
+            const int lim = !key_ok ? 1 << 30 : (causal ? key - q0 - 4 * g2 : -1);
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const f32x4 lv = *reinterpret_cast<const f32x4*>(&Ls[b][8 * a + 4 * g2]);
-                const f32x4 dv4 = *reinterpret_cast<const f32x4*>(&Ds[b][8 * a + 4 * g2]);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int r = 4 * a + u;
-                    float p = fast_exp2(fmaf(s[r], c, -lv[u]));
-                    if (masked && (!key_ok || (causal && key > q0 + 8 * a + 4 * g2 + u)))
-                        p = 0.0f;
-                    s[r] = p;
-                    dp[r] = p * (dp[r] - dv4[u]);
-                }
-            }
-            // dV^T += dO^T P and dK^T += Q^T dS: k = the block's query rows.
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const frag bp = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
-                                             s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
-                const frag bs = pack_frag<T>(dp[8 * j + 0], dp[8 * j + 1], dp[8 * j + 2],
-                                             dp[8 * j + 3], dp[8 * j + 4], dp[8 * j + 5],
-                                             dp[8 * j + 6], dp[8 * j + 7]);
-#pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) {
-                    dv[dt] = Elem<T>::mma(
-                        read_tr_frag<T>(&Oc[b][16 * j * CP + 32 * dt + tr_c], CP), bp, dv[dt]);
-                    dk[dt] = Elem<T>::mma(
-                        read_tr_frag<T>(&Qc[b][16 * j * CP + 32 * dt + tr_c], CP), bs, dk[dt]);
-                }
-            }
+            for (int r = 0; r < 16; ++r)
+                s[r] = (8 * (r >> 2) + (r & 3) < lim) ? -INFINITY : s[r];
         }
-        // dS^T[key][q], rounded to T.
+        frag bp[2], bs[2];
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-            u32x2 w;
-            w[0] = Elem<T>::pack2(dp[4 * a + 0], dp[4 * a + 1]);
-            w[1] = Elem<T>::pack2(dp[4 * a + 2], dp[4 * a + 3]);
-            st8(&St[b][(32 * wave + l32) * SP + 8 * a + 4 * g2], w);
-        }
-        if (qb + 1 < nqb) {
-            stage(b ^ 1);
-            if (qb + 2 < nqb) fetch(qb + 2);
-        }
-        __syncthreads();
-
-        // dQ[q0 : q0+32, 32*dtile : +32] += dS K over this wave's share of the keys.
-        f32x16 acc = f32x16{};
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2]);
+            const f32x4 y = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2 + 2]);
+            const float lv[4] = {x[0], x[2], y[0], y[2]};
+            const float dd[4] = {x[1], x[3], y[1], y[3]};
 #pragma unroll
-        for (int jj = 0; jj < Cfg::KSTEPS; ++jj) {
-            const int j = jbeg + jj;
-            const frag a = read_tr_frag<T>(&St[b][16 * j * SP + tr_s], SP);
-            const frag bk = read_tr_frag<T>(&Kc[16 * j * CP + 32 * dtile + tr_c], CP);
-            acc = Elem<T>::mma(a, bk, acc);
+            for (int k2 = 0; k2 < 4; ++k2) {
+                const int r = 4 * a + k2;
+                const float p = fast_exp2(fmaf(s[r], cs, -lv[k2]));
+                s[r] = p;
+                dp[r] = p * (dp[r] - dd[k2]);
+            }
         }
-        dq_prev = acc;
-        q0_prev = q0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            bp[j] = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
+                                 s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
+            bs[j] = pack_frag<T>(dp[8 * j + 0], dp[8 * j + 1], dp[8 * j + 2], dp[8 * j + 3],
+                                 dp[8 * j + 4], dp[8 * j + 5], dp[8 * j + 6], dp[8 * j + 7]);
+        }
+        // dV^T += dO^T P and dK^T += Q^T dS (k = the block's 32 query rows).
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const unsigned char* oa = ot + tr_off + j * 4 * GRP + dt * 256;
+                const unsigned char* qa = qt + tr_off + j * 4 * GRP + dt * 256;
+                dv[dt] = Elem<T>::mma(tr_frag_at<T>(oa, oa + 2 * GRP), bp[j], dv[dt]);
+                dk[dt] = Elem<T>::mma(tr_frag_at<T>(qa, qa + 2 * GRP), bs[j], dk[dt]);
+            }
+        }
     }
-    flush_dq();
 
     if (key_ok) {
         uint16_t* krow = dK + head + static_cast<size_t>(key) * D;
@@ -681,21 +632,130 @@ __global__ void __launch_bounds__(256, 1)
     }
 }
 
-// dQ = T(scale * dq_acc), eight elements per thread.
 template <typename T>
-__global__ void __launch_bounds__(256)
-    dq_convert_kernel(const float* __restrict__ acc, uint16_t* __restrict__ dQ, float scale,
-                      long long n8) {
-    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const f32x4 a = __builtin_bit_cast(f32x4, ld16(acc + 8 * i));
-    const f32x4 b = __builtin_bit_cast(f32x4, ld16(acc + 8 * i + 4));
-    u32x4 w;
-    w[0] = Elem<T>::pack2(a[0] * scale, a[1] * scale);
-    w[1] = Elem<T>::pack2(a[2] * scale, a[3] * scale);
-    w[2] = Elem<T>::pack2(b[0] * scale, b[1] * scale);
-    w[3] = Elem<T>::pack2(b[2] * scale, b[3] * scale);
-    st16(dQ + 8 * i, w);
+__global__ void __launch_bounds__(256, 2)
+    dq_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                   const uint16_t* __restrict__ V, const float2* __restrict__ LD,
+                   const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ, int N, int Npad,
+                   int nqb, float c, float scale, int causal) {
+    constexpr int D = 128;
+    constexpr int BM = 128;  // query rows per workgroup (32 per wave)
+    constexpr int BN = 32;   // keys per block
+    constexpr int GRP = kGrp128;
+    constexpr int KT = (BN / 4) * GRP;
+    constexpr int SET = 2 * KT;  // K tile, V tile
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * SET];
+
+    int bh, rank;
+    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * N * D;
+    const uint16_t* Kh = K + head;
+    const uint16_t* Vh = V + head;
+    const int q0 = qb * BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;              // query row owned by this lane
+    const bool q_ok = q < N;
+
+    // Q^T and dO^T as B operands of S^T = K Q^T and dP^T = V dO^T (k = d).
+    frag qf[D / 16];
+    frag of[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4 qv = {0u, 0u, 0u, 0u}, ov = {0u, 0u, 0u, 0u};
+        if (q_ok) {
+            qv = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+            ov = ld16(dO + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        }
+        qf[ks] = as_frag<T>(qv);
+        of[ks] = as_frag<T>(ov);
+    }
+    // (L log2 e, D) of this lane's query; padding rows give P = 0.
+    const float2 ldq = (q < Npad) ? LD[static_cast<size_t>(bh) * Npad + q] : make_float2(INFINITY, 0.0f);
+
+    const int ld_row = lane & 3;
+    const int ld_col = (lane >> 2) * 8;
+    auto load_block = [&](int kb, int b) {
+        const int r0 = kb * BN;
+        unsigned char* set = smem + b * SET;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int grp = wave + 4 * i;
+            const int row = min(r0 + 4 * grp + ld_row, N - 1);
+            lds_dma16_async(Kh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
+            lds_dma16_async(Vh + static_cast<size_t>(row) * D + ld_col, set + KT + grp * GRP);
+        }
+    };
+    const int row_off = grp_row_off();
+    const int tr_off = g2 * GRP + grp_tr_sub();
+
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    const float cs = fmaxf(c, kFltMin);
+    const int kv_end = causal ? min(N, (qb + 1) * BM) : N;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    load_block(0, 0);
+    int b = 0;
+    for (int kb = 0; kb < nkb; ++kb, b ^= 1) {
+        const int key0 = kb * BN;
+        __builtin_amdgcn_s_waitcnt(0);  // block kb is in LDS
+        __syncthreads();                // ... for every wave; block kb - 1 is no longer read
+        if (kb + 1 < nkb) load_block(kb + 1, b ^ 1);
+        const unsigned char* kt = smem + b * SET;
+        const unsigned char* vt = kt + KT;
+
+        // S^T = K Q^T and dP^T = V dO^T: rows = keys, lane = query.
+        f32x16 s = f32x16{};
+        f32x16 dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+            s = Elem<T>::mma(as_frag<T>(ld16(kt + row_off + ks * 128)), qf[ks], s);
+            dp = Elem<T>::mma(as_frag<T>(ld16(vt + row_off + ks * 128)), of[ks], dp);
+        }
+        if (key0 + BN > N || (causal && key0 + BN - 1 > q0)) {
+            const int lim = min(N, causal ? q + 1 : N) - key0 - 4 * g2;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                s[r] = (8 * (r >> 2) + (r & 3) < lim) ? s[r] : -INFINITY;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(fmaf(s[r], cs, -ldq.x));
+            s[r] = p * (dp[r] - ldq.y);  // dS^T
+        }
+        // dQ^T += K^T dS^T (k = the block's 32 keys; K^T by transpose reads).
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const frag bsf = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
+                                          s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const unsigned char* ka = kt + tr_off + j * 4 * GRP + dt * 256;
+                acc[dt] = Elem<T>::mma(tr_frag_at<T>(ka, ka + 2 * GRP), bsf, acc[dt]);
+            }
+        }
+    }
+
+    if (q_ok) {
+        uint16_t* row = dQ + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                u32x2 w;
+                w[0] = Elem<T>::pack2(acc[dt][4 * a + 0] * scale, acc[dt][4 * a + 1] * scale);
+                w[1] = Elem<T>::pack2(acc[dt][4 * a + 2] * scale, acc[dt][4 * a + 3] * scale);
+                st8(row + 32 * dt + 8 * a + 4 * g2, w);
+            }
+        }
+    }
 }
 
 }  // namespace dev
@@ -704,7 +764,7 @@ namespace detail {
 
 namespace {
 
-// Deterministic path: delta, dq_kernel, dkdv_kernel (no atomics; dQ recomputes S and dP).
+// Generic path (fp32, and head_dim 32 / 64): delta, dq_kernel, dkdv_kernel.
 template <typename T, int D>
 FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, const T* O,
                                           const float* L, const T* dO, T* dQ, T* dK, T* dV,
@@ -730,7 +790,7 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     if (dblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     int tok = profile_kernel<T, D>("backward_delta", stream);
     hipLaunchKernelGGL((dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
-                       0, stream, go, o, delta, nullptr, rows);
+                       0, stream, go, o, delta, rows);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
@@ -765,77 +825,64 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     return err;
 }
 
-// Fused path (fp16 / bf16): delta (+ clear the fp32 dQ accumulator), bwd_fused_kernel,
-// dq_convert_kernel. dQ is summed with fp32 atomics, so its last bit may differ between runs.
-template <typename T, int D>
-FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const T* O,
-                                       const float* L, const T* dO, T* dQ, T* dK, T* dV, int BH,
-                                       int N, float scale, bool causal, hipStream_t stream) {
+// Two-pass path for head_dim 128: delta_ld_kernel, dq_d128_kernel, dkdv_d128_kernel.
+template <typename T>
+FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* V, const T* O,
+                                               const float* L, const T* dO, T* dQ, T* dK, T* dV,
+                                               int BH, int N, float scale, bool causal,
+                                               hipStream_t stream) {
+    constexpr int D = 128;
+    const int Npad = (N + 31) / 32 * 32;
+    const long long rows_pad = static_cast<long long>(BH) * Npad;
+    StreamWorkspace ws(stream);
+    FlashAttentionError err = ws.alloc(static_cast<size_t>(rows_pad) * sizeof(float2));
+    if (err != FlashAttentionError::SUCCESS) return err;
+    float2* ld = static_cast<float2*>(ws.get());
+
+    const long long dblocks = (rows_pad * (D / 8) + 255) / 256;
+    const int nqb = (N + 127) / 128;
+    const int nkb = (N + 127) / 128;
+    const long long qblocks = static_cast<long long>(nqb) * BH;
+    const long long kblocks = static_cast<long long>(nkb) * BH;
+    if (dblocks > 0x7fffffffLL || qblocks > 0x7fffffffLL || kblocks > 0x7fffffffLL)
+        return FlashAttentionError::INVALID_DIMENSION;
+    const float c = scale * dev::kLog2e;
     const uint16_t* q = reinterpret_cast<const uint16_t*>(Q);
     const uint16_t* k = reinterpret_cast<const uint16_t*>(K);
     const uint16_t* v = reinterpret_cast<const uint16_t*>(V);
-    const uint16_t* o = reinterpret_cast<const uint16_t*>(O);
     const uint16_t* go = reinterpret_cast<const uint16_t*>(dO);
 
-    const long long rows = static_cast<long long>(BH) * N;
-    // delta (rows floats, padded to 256 bytes) followed by the dQ accumulator (rows * D floats).
-    const size_t delta_bytes = (static_cast<size_t>(rows) * sizeof(float) + 255) & ~size_t(255);
-    const size_t acc_bytes = static_cast<size_t>(rows) * D * sizeof(float);
-    StreamWorkspace ws(stream);
-    FlashAttentionError err = ws.alloc(delta_bytes + acc_bytes);
-    if (err != FlashAttentionError::SUCCESS) return err;
-    float* delta = static_cast<float*>(ws.get());
-    float* dq_acc = reinterpret_cast<float*>(static_cast<char*>(ws.get()) + delta_bytes);
-
-    constexpr int LPR = D / 8;
-    const long long dblocks = (rows * LPR + 255) / 256;
-    using Cfg = dev::FusedCfg<D>;
-    const int nkb = (N + Cfg::BN - 1) / Cfg::BN;
-    const long long blocks = static_cast<long long>(nkb) * BH;
-    const long long n8 = rows * D / 8;
-    const long long cblocks = (n8 + 255) / 256;
-    if (dblocks > 0x7fffffffLL || blocks > 0x7fffffffLL || cblocks > 0x7fffffffLL)
-        return FlashAttentionError::INVALID_DIMENSION;
-
     int tok = profile_kernel<T, D>("backward_delta", stream);
-    hipLaunchKernelGGL((dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
-                       0, stream, go, o, delta, dq_acc, rows);
+    hipLaunchKernelGGL((dev::delta_ld_kernel<T>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
+                       0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, N, Npad,
+                       rows_pad);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
-    tok = profile_kernel<T, D>("backward_fused", stream);
-    hipLaunchKernelGGL((dev::bwd_fused_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta, dq_acc,
-                       reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), N, nkb,
-                       scale * dev::kLog2e, scale, causal ? 1 : 0);
+    tok = profile_kernel<T, D>("backward_dq", stream);
+    hipLaunchKernelGGL((dev::dq_d128_kernel<T>), dim3(static_cast<unsigned>(qblocks)), dim3(256), 0,
+                       stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ), N, Npad, nqb, c,
+                       scale, causal ? 1 : 0);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
-    tok = profile_kernel<T, D>("backward_dq_convert", stream);
-    hipLaunchKernelGGL((dev::dq_convert_kernel<T>), dim3(static_cast<unsigned>(cblocks)),
-                       dim3(256), 0, stream, dq_acc, reinterpret_cast<uint16_t*>(dQ), scale, n8);
+    tok = profile_kernel<T, D>("backward_dkdv", stream);
+    hipLaunchKernelGGL((dev::dkdv_d128_kernel<T>), dim3(static_cast<unsigned>(kblocks)), dim3(256),
+                       0, stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dK),
+                       reinterpret_cast<uint16_t*>(dV), N, Npad, nkb, c, scale, causal ? 1 : 0);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
-}
-
-// CUFLASH_DETERMINISTIC=1 in the environment selects the atomic-free two-pass backward for
-// fp16 / bf16 as well (read on every call).
-bool deterministic_requested() {
-    const char* e = std::getenv("CUFLASH_DETERMINISTIC");
-    return e && e[0] && !(e[0] == '0' && e[1] == '\0');
 }
 
 template <typename T, int D>
 FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O, const float* L,
                                  const T* dO, T* dQ, T* dK, T* dV, int BH, int N, float scale,
                                  bool causal, hipStream_t stream) {
-    if constexpr (!std::is_same<T, float>::value) {
-        if (!deterministic_requested())
-            return run_backward_fused<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, BH, N, scale, causal,
-                                            stream);
-    }
+    if constexpr (!std::is_same<T, float>::value && D == 128)
+        return run_backward_two_pass_d128<T>(Q, K, V, O, L, dO, dQ, dK, dV, BH, N, scale, causal,
+                                             stream);
     return run_backward_two_pass<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, BH, N, scale, causal,
                                        stream);
 }

@@ -246,6 +246,29 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned char* lds_ba
                                      0, 0);
 }
 
+// The same loads issued from inline assembly. The compiler then does not know that they write
+// LDS and adds no waits for them, so the kernel must order every LDS access itself
+// (s_waitcnt vmcnt(0) and a barrier before the data is read, and before a buffer is reused).
+// This lets a kernel rotate buffers with run-time offsets, where the compiler would otherwise
+// wait for every outstanding load before each LDS read. An SALU write of M0 needs one wait state
+// before an LDS DMA that uses it (the s_nop); M0 has no other user in these kernels.
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+    return static_cast<unsigned>(reinterpret_cast<uintptr_t>(
+        (const __attribute__((address_space(3))) unsigned char*)(p)));
+}
+__device__ __forceinline__ void lds_dma16_async(const void* src, unsigned char* lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma4_async(const void* src, unsigned char* lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "memory");
+}
+
 // ---------------------------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------------------------
