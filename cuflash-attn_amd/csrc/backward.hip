@@ -563,13 +563,31 @@ __global__ void __launch_bounds__(256, 2)
         const unsigned char* ot = qt + QT;
         const float2* ldv = reinterpret_cast<const float2*>(qt + 2 * QT);
 
-        // S = Q K^T and dP = dO V^T: rows = queries, lane = key.
+        // S = Q K^T and dP = dO V^T: rows = queries, lane = key. Operand i (i even: Q, odd: dO;
+        // k-step i / 2) is read kAhead MFMAs before its product; the scheduling fences keep the
+        // compiler from undoing that order.
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
+        {
+            constexpr int kAhead = 3;
+            frag fa[16];
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-            s = Elem<T>::mma(as_frag<T>(ld16(qt + row_off + ks * 128)), kf[ks], s);
-            dp = Elem<T>::mma(as_frag<T>(ld16(ot + row_off + ks * 128)), vf[ks], dp);
+            for (int i = 0; i < 16; ++i) {
+                if (i == 0) {
+#pragma unroll
+                    for (int k = 0; k < kAhead; ++k)
+                        fa[k] = as_frag<T>(ld16((k & 1 ? ot : qt) + row_off + (k >> 1) * 128));
+                }
+                if (i + kAhead < 16) {
+                    const int k = i + kAhead;
+                    fa[k] = as_frag<T>(ld16((k & 1 ? ot : qt) + row_off + (k >> 1) * 128));
+                }
+                if (i & 1)
+                    dp = Elem<T>::mma(fa[i], vf[i >> 1], dp);
+                else
+                    s = Elem<T>::mma(fa[i], kf[i >> 1], s);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if ((causal && k0 + 31 > q0) || k0 + 31 >= N) {
             const int lim = !key_ok ? 1 << 30 : (causal ? key - q0 - 4 * g2 : -1);
@@ -599,15 +617,30 @@ __global__ void __launch_bounds__(256, 2)
             bs[j] = pack_frag<T>(dp[8 * j + 0], dp[8 * j + 1], dp[8 * j + 2], dp[8 * j + 3],
                                  dp[8 * j + 4], dp[8 * j + 5], dp[8 * j + 6], dp[8 * j + 7]);
         }
-        // dV^T += dO^T P and dK^T += Q^T dS (k = the block's 32 query rows).
+        // dV^T += dO^T P and dK^T += Q^T dS (k = the block's 32 query rows). Operand i
+        // (j = i / 8, dt = (i / 2) % 4; even: dO^T, odd: Q^T) is read kAhead MFMAs ahead.
+        {
+            constexpr int kAhead = 3;
+            frag fa[16];
+            auto operand = [&](int i) {
+                const unsigned char* a =
+                    (i & 1 ? qt : ot) + tr_off + (i >> 3) * 4 * GRP + ((i >> 1) & 3) * 256;
+                return tr_frag_at<T>(a, a + 2 * GRP);
+            };
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+            for (int i = 0; i < 16; ++i) {
+                if (i == 0) {
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const unsigned char* oa = ot + tr_off + j * 4 * GRP + dt * 256;
-                const unsigned char* qa = qt + tr_off + j * 4 * GRP + dt * 256;
-                dv[dt] = Elem<T>::mma(tr_frag_at<T>(oa, oa + 2 * GRP), bp[j], dv[dt]);
-                dk[dt] = Elem<T>::mma(tr_frag_at<T>(qa, qa + 2 * GRP), bs[j], dk[dt]);
+                    for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
+                }
+                if (i + kAhead < 16) fa[i + kAhead] = operand(i + kAhead);
+                const int j = i >> 3;
+                const int dt = (i >> 1) & 3;
+                if (i & 1)
+                    dk[dt] = Elem<T>::mma(fa[i], bs[j], dk[dt]);
+                else
+                    dv[dt] = Elem<T>::mma(fa[i], bp[j], dv[dt]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
@@ -711,13 +744,30 @@ __global__ void __launch_bounds__(256, 2)
         const unsigned char* kt = smem + b * SET;
         const unsigned char* vt = kt + KT;
 
-        // S^T = K Q^T and dP^T = V dO^T: rows = keys, lane = query.
+        // S^T = K Q^T and dP^T = V dO^T: rows = keys, lane = query. Operand i (even: K, odd:
+        // V; k-step i / 2) is read kAhead MFMAs before its product.
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
+        {
+            constexpr int kAhead = 3;
+            frag fa[16];
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-            s = Elem<T>::mma(as_frag<T>(ld16(kt + row_off + ks * 128)), qf[ks], s);
-            dp = Elem<T>::mma(as_frag<T>(ld16(vt + row_off + ks * 128)), of[ks], dp);
+            for (int i = 0; i < 16; ++i) {
+                if (i == 0) {
+#pragma unroll
+                    for (int k = 0; k < kAhead; ++k)
+                        fa[k] = as_frag<T>(ld16((k & 1 ? vt : kt) + row_off + (k >> 1) * 128));
+                }
+                if (i + kAhead < 16) {
+                    const int k = i + kAhead;
+                    fa[k] = as_frag<T>(ld16((k & 1 ? vt : kt) + row_off + (k >> 1) * 128));
+                }
+                if (i & 1)
+                    dp = Elem<T>::mma(fa[i], of[i >> 1], dp);
+                else
+                    s = Elem<T>::mma(fa[i], qf[i >> 1], s);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (key0 + BN > N || (causal && key0 + BN - 1 > q0)) {
             const int lim = min(N, causal ? q + 1 : N) - key0 - 4 * g2;
@@ -730,15 +780,29 @@ __global__ void __launch_bounds__(256, 2)
             const float p = fast_exp2(fmaf(s[r], cs, -ldq.x));
             s[r] = p * (dp[r] - ldq.y);  // dS^T
         }
-        // dQ^T += K^T dS^T (k = the block's 32 keys; K^T by transpose reads).
+        // dQ^T += K^T dS^T (k = the block's 32 keys; K^T by transpose reads). Operand i
+        // (j = i / 4, dt = i % 4) is read kAhead MFMAs ahead.
+        {
+            frag bsf[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const frag bsf = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
-                                          s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
+            for (int j = 0; j < 2; ++j)
+                bsf[j] = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
+                                      s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
+            constexpr int kAhead = 3;
+            frag fa[8];
+            auto operand = [&](int i) {
+                const unsigned char* a = kt + tr_off + (i >> 2) * 4 * GRP + (i & 3) * 256;
+                return tr_frag_at<T>(a, a + 2 * GRP);
+            };
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const unsigned char* ka = kt + tr_off + j * 4 * GRP + dt * 256;
-                acc[dt] = Elem<T>::mma(tr_frag_at<T>(ka, ka + 2 * GRP), bsf, acc[dt]);
+            for (int i = 0; i < 8; ++i) {
+                if (i == 0) {
+#pragma unroll
+                    for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
+                }
+                if (i + kAhead < 8) fa[i + kAhead] = operand(i + kAhead);
+                acc[i & 3] = Elem<T>::mma(fa[i], bsf[i >> 2], acc[i & 3]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
