@@ -199,10 +199,10 @@ def main():
     value = (f_fwd + f_bwd) / (ms_per_step * 1e-3) / 1e12
 
     # Algorithmic FLOPs per launch: forward = F_fwd; F_bwd counts five N^2 products (S, dP, dV,
-    # dK, dQ). The fused backward performs all five once (F_bwd). The deterministic two-pass
-    # backward splits them: dkdv performs S, dP, dV, dK (4/5 of F_bwd), dq performs dQ (1/5)
-    # plus a recompute of S and dP that the algorithmic count does not include.
-    alg = {"forward": f_fwd, "backward_fused": f_bwd, "backward_dq": f_bwd / 5,
+    # dK, dQ). The backward runs its dkdv part (S, dP, dV, dK: 4/5 of F_bwd) and its dq part (dQ:
+    # 1/5, plus a recompute of S and dP that the algorithmic count does not include) either in
+    # one launch (backward_dq_dkdv, head_dim 128) or as two kernels.
+    alg = {"forward": f_fwd, "backward_dq_dkdv": f_bwd, "backward_dq": f_bwd / 5,
            "backward_dkdv": f_bwd * 4 / 5}
     suffix = f"_bf16_d{D}"
     k_ms = {label[:-len(suffix)]: tot / n for label, (n, tot) in kernels.items()

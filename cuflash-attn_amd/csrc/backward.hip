@@ -18,8 +18,8 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
-// For fp16/bf16 at head_dim 128 the same three steps run as delta_ld_kernel, dq_d128_kernel
-// and dkdv_d128_kernel (section 4). Every path is deterministic: no atomics, and each output
+// For fp16/bf16 at head_dim 128 the same steps run as delta_ld_kernel, then dq_d128 and
+// dkdv_d128 side by side in one launch (bwd_d128_kernel, section 4). Every path is deterministic: no atomics, and each output
 // element is written by exactly one lane.
 
 #include "common.hpp"
@@ -457,7 +457,7 @@ __global__ void __launch_bounds__(256)
 }
 
 // ------------------------------------------------------------------------------------------
-// dkdv_d128_kernel and dq_d128_kernel restate dkdv_kernel and dq_kernel (same products, same
+// dkdv_d128 and dq_d128 restate dkdv_kernel and dq_kernel (same products, same
 // rounding of P and dS to T) with a gfx950 data path: tiles go global -> LDS by direct loads
 // (global_load_lds_dwordx4, issued from inline assembly so that buffers can rotate at run time)
 // into the padded 4-row-group layout of fwd16_d128_kernel, whose single copy of a tile serves
@@ -479,24 +479,29 @@ __device__ __forceinline__ int grp_tr_sub() {  // transpose reads, without the r
     return (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 + (kq & 1) * 8;
 }
 
+// Key-stationary part of workgroup `bid` of BH * nkb (kb = 0, the most work, first); smem
+// holds at least kDkdvLds bytes.
+constexpr int kDkdvLds = 2 * (2 * 8 * kGrp128 + 32 * 8);
 template <typename T>
-__global__ void __launch_bounds__(256, 2)
-    dkdv_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
-                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dK,
-                     uint16_t* __restrict__ dV, int N, int Npad, int nkb, float c, float scale,
-                     int causal) {
+__device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
+                                          const uint16_t* __restrict__ K,
+                                          const uint16_t* __restrict__ V,
+                                          const float2* __restrict__ LD,
+                                          const uint16_t* __restrict__ dO,
+                                          uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                                          int N, int Npad, int nkb, int BH, float c, float scale,
+                                          int causal, int bid, unsigned char* smem) {
     constexpr int D = 128;
     constexpr int BN = 128;  // keys per workgroup (32 per wave)
     constexpr int BM = 32;   // query rows per block
     constexpr int GRP = kGrp128;
     constexpr int QT = (BM / 4) * GRP;
     constexpr int SET = 2 * QT + BM * 8;  // Q tile, dO tile, 32 x (L, D)
+    static_assert(2 * SET == kDkdvLds, "LDS size");
     using frag = typename Elem<T>::frag;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * SET];
 
     int bh, kb;
-    head_rank_order(blockIdx.x, gridDim.x / nkb, bh, kb);  // kb = 0 (most work) first
+    head_rank_order(bid, BH, bh, kb);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31;
@@ -665,23 +670,29 @@ __global__ void __launch_bounds__(256, 2)
     }
 }
 
+// Query-stationary part of workgroup `bid` of BH * nqb (causal: the longest query blocks
+// first); smem holds at least kDqLds bytes.
+constexpr int kDqLds = 2 * 2 * 8 * kGrp128;
 template <typename T>
-__global__ void __launch_bounds__(256, 2)
-    dq_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                   const uint16_t* __restrict__ V, const float2* __restrict__ LD,
-                   const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ, int N, int Npad,
-                   int nqb, float c, float scale, int causal) {
+__device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
+                                        const uint16_t* __restrict__ K,
+                                        const uint16_t* __restrict__ V,
+                                        const float2* __restrict__ LD,
+                                        const uint16_t* __restrict__ dO,
+                                        uint16_t* __restrict__ dQ, int N, int Npad, int nqb,
+                                        int BH, float c, float scale, int causal, int bid,
+                                        unsigned char* smem) {
     constexpr int D = 128;
     constexpr int BM = 128;  // query rows per workgroup (32 per wave)
     constexpr int BN = 32;   // keys per block
     constexpr int GRP = kGrp128;
     constexpr int KT = (BN / 4) * GRP;
     constexpr int SET = 2 * KT;  // K tile, V tile
+    static_assert(2 * SET == kDqLds, "LDS size");
     using frag = typename Elem<T>::frag;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * SET];
 
     int bh, rank;
-    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    head_rank_order(bid, BH, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -822,6 +833,30 @@ __global__ void __launch_bounds__(256, 2)
     }
 }
 
+// One launch for both passes (they are independent once delta_ld_kernel has run): workgroup
+// ids alternate between the dq and the dkdv grid, each in its own longest-first order, so the
+// two halves share the machine and their tails overlap instead of adding a kernel boundary.
+template <typename T>
+__global__ void __launch_bounds__(256, 2)
+    bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                    const uint16_t* __restrict__ V, const float2* __restrict__ LD,
+                    const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
+                    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int N, int Npad, int nb,
+                    int BH, float c, float scale, int causal) {
+    constexpr int kLds = kDkdvLds > kDqLds ? kDkdvLds : kDqLds;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
+    // nb query blocks of 128 rows = nb key blocks of 128 keys per head.
+    const int half = BH * nb;
+    const int bid = blockIdx.x;
+    if (bid < 2 * half) {  // interleaved part
+        if (bid & 1)
+            dq_d128<T>(Q, K, V, LD, dO, dQ, N, Npad, nb, BH, c, scale, causal, bid >> 1, smem);
+        else
+            dkdv_d128<T>(Q, K, V, LD, dO, dK, dV, N, Npad, nb, BH, c, scale, causal, bid >> 1,
+                         smem);
+    }
+}
+
 }  // namespace dev
 
 namespace detail {
@@ -889,7 +924,7 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     return err;
 }
 
-// Two-pass path for head_dim 128: delta_ld_kernel, dq_d128_kernel, dkdv_d128_kernel.
+// Path for head_dim 128: delta_ld_kernel, then bwd_d128_kernel (dq and dkdv in one launch).
 template <typename T>
 FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* V, const T* O,
                                                const float* L, const T* dO, T* dQ, T* dK, T* dV,
@@ -908,7 +943,7 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     const int nkb = (N + 127) / 128;
     const long long qblocks = static_cast<long long>(nqb) * BH;
     const long long kblocks = static_cast<long long>(nkb) * BH;
-    if (dblocks > 0x7fffffffLL || qblocks > 0x7fffffffLL || kblocks > 0x7fffffffLL)
+    if (dblocks > 0x7fffffffLL || qblocks + kblocks > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
     const float c = scale * dev::kLog2e;
     const uint16_t* q = reinterpret_cast<const uint16_t*>(Q);
@@ -924,18 +959,11 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
-    tok = profile_kernel<T, D>("backward_dq", stream);
-    hipLaunchKernelGGL((dev::dq_d128_kernel<T>), dim3(static_cast<unsigned>(qblocks)), dim3(256), 0,
-                       stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ), N, Npad, nqb, c,
-                       scale, causal ? 1 : 0);
-    profile_end(tok, stream);
-    err = from_hip(hipGetLastError());
-    if (err != FlashAttentionError::SUCCESS) return err;
-
-    tok = profile_kernel<T, D>("backward_dkdv", stream);
-    hipLaunchKernelGGL((dev::dkdv_d128_kernel<T>), dim3(static_cast<unsigned>(kblocks)), dim3(256),
-                       0, stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dK),
-                       reinterpret_cast<uint16_t*>(dV), N, Npad, nkb, c, scale, causal ? 1 : 0);
+    tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
+    hipLaunchKernelGGL((dev::bwd_d128_kernel<T>), dim3(static_cast<unsigned>(qblocks + kblocks)),
+                       dim3(256), 0, stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ),
+                       reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), N, Npad,
+                       nqb, BH, c, scale, causal ? 1 : 0);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
