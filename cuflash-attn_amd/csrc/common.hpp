@@ -58,6 +58,12 @@ struct Elem<__hip_bfloat16> {
     static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
+    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_bf16 with (1, 1)).
+    static __device__ __forceinline__ float sum2(uint32_t v, float acc) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v),
+                                               __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
+    }
 };
 
 template <>
@@ -73,6 +79,12 @@ struct Elem<__half> {
     }
     static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_f16 with (1, 1)).
+    static __device__ __forceinline__ float sum2(uint32_t v, float acc) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, v),
+                                      __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
     }
 };
 
@@ -260,6 +272,17 @@ __device__ __forceinline__ void lds_dma16_async(const void* src, unsigned char* 
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "memory");
+}
+// The same load with a wave-uniform base address in SGPRs and a 32-bit per-lane byte offset:
+// the address of lane i is sbase + voff(i), so a kernel that streams tiles keeps voff fixed and
+// only advances sbase (scalar adds) from tile to tile.
+__device__ __forceinline__ void lds_dma16_async_s(const void* sbase, unsigned voff,
+                                                  unsigned char* lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase),
+                   "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
                  : "memory");
 }
 __device__ __forceinline__ void lds_dma4_async(const void* src, unsigned char* lds_base) {

@@ -193,8 +193,12 @@ __global__ void __launch_bounds__(256, 2)
 // ------------------------------------------------------------------------------------------
 // fp16 / bf16 kernel for head_dim 128 (the headline shape), software-pipelined
 // ------------------------------------------------------------------------------------------
-// Same decomposition and numerics as fwd16_kernel (128 query rows per workgroup, 32 per wave,
-// S^T = K Q^T with Q^T in registers, O^T += V^T P^T), restructured for gfx950:
+// Same per-wave decomposition as fwd16_kernel (32 query rows per wave, S^T = K Q^T with Q^T in
+// registers, O^T += V^T P^T), restructured for gfx950:
+//  * a workgroup holds NW waves (32 NW query rows) and one workgroup runs per CU for NW = 8:
+//    the K/V tiles a workgroup loads are shared by all its waves, and a CU's vector memory
+//    path (about 64 bytes per clock) is the limit of the tile loads, so the larger workgroup
+//    halves the load time per MFMA compared with two workgroups of four waves;
 //  * K and V blocks of 64 keys go global -> LDS with global_load_lds_dwordx4 (no staging
 //    registers, no VALU or ds_write for the copy) into double buffers, so one barrier per block
 //    suffices and the next blocks load while the current one is consumed;
@@ -207,14 +211,15 @@ __global__ void __launch_bounds__(256, 2)
 //  * the scores of block j+1 are formed by MFMA while the softmax of block j runs on the VALU
 //    (two score register sets), and P V of block j follows;
 //  * the lane-pair row max / sum use v_permlane32_swap instead of an LDS permute.
-template <typename T>
-__global__ void __launch_bounds__(256, 2)
+template <typename T, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW)
     fwd16_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                       float* __restrict__ L, int N, int nqb, float c, int causal) {
     constexpr int D = 128;
-    constexpr int BM = 128;
+    constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
     constexpr int BN = 64;
+    constexpr int kParts = 16 / NW;  // load instructions per wave per 64-row tile
     constexpr int GRP = 1088;              // bytes per 4-row group
     constexpr int TILE = (BN / 4) * GRP;   // bytes per 64-row tile
     using frag = typename Elem<T>::frag;
@@ -249,17 +254,29 @@ __global__ void __launch_bounds__(256, 2)
     const int kv_end = causal ? min(N, (qb + 1) * BM) : N;
     const int nkb = (kv_end + BN - 1) / BN;
 
-    // Loads of one 64-row tile: wave w fills groups w, w + 4, w + 8, w + 12. Rows past N are
-    // clamped to row N - 1 (finite values; their scores are masked).
+    // Loads of one 64-row tile: wave w fills groups w, w + NW, ... (kParts of them). Rows past
+    // N are clamped to row N - 1 (finite values; their scores are masked). The loads are issued from
+    // inline assembly, so the compiler adds no waits for them and keeps partial LDS waits for
+    // the operand reads; the loop orders every LDS access itself (s_waitcnt(0) and a barrier
+    // before a tile is read and before a buffer is refilled).
+    // A tile that lies inside [0, N) is addressed as a scalar base plus a fixed per-lane offset.
     const int ld_row = lane & 3;
     const int ld_col = (lane >> 2) * 8;
+    const unsigned ld_voff = static_cast<unsigned>(((4 * wave + ld_row) * D + ld_col) * 2);
+    // Part i (0..kParts-1) of a tile load: this wave's group wave + NW i.
+    auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
+        if (key0 + BN <= N) {
+            lds_dma16_async_s(src + static_cast<size_t>(key0 + 4 * NW * i) * D, ld_voff,
+                              dst + (wave + NW * i) * GRP);
+        } else {
+            const int grp = wave + NW * i;
+            const int row = min(key0 + 4 * grp + ld_row, N - 1);
+            lds_dma16_async(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
+        }
+    };
     auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int grp = wave + 4 * i;
-            const int row = min(key0 + 4 * grp + ld_row, N - 1);
-            lds_dma16(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
-        }
+        for (int i = 0; i < kParts; ++i) load_part(src, key0, dst, i);
     };
     // Per-lane byte offsets of the operand reads (see the layout above).
     const int k_off = (l32 >> 2) * GRP + g2 * 64 + (l32 & 3) * 16;
@@ -300,17 +317,12 @@ __global__ void __launch_bounds__(256, 2)
         }
     };
 
-    // Row max of one block and the online-softmax update of (m, l). Returns whether some lane
-    // of the wave must rescale its O by alpha. The lazy rescale is decided per lane with
-    // selects: m only moves when the block max exceeds it by more than kLazyRescale, and O and
-    // l of that lane are scaled by the same alpha, so the result is exact either way.
-    auto update_max = [&](const f32x16 (&s)[2], float& alpha) -> bool {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-        }
+    // Online-softmax update of (m, l) from mx, this lane's raw row max of the next block.
+    // Returns whether some lane of the wave must rescale its O by alpha. The lazy rescale is
+    // decided per lane with selects: m only moves when the block max exceeds it by more than
+    // kLazyRescale, and O and l of that lane are scaled by the same alpha, so the result is
+    // exact either way.
+    auto update_max = [&](float mx, float& alpha) -> bool {
         const float m_new = fmaxf(m, pair_max(mx) * cs);
         const bool grow = m_new > m + kLazyRescale;
         const float a_raw = fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new);
@@ -320,62 +332,113 @@ __global__ void __launch_bounds__(256, 2)
         return __ballot(grow) != 0;
     };
 
-    // One pipelined step, free of branches so that the scheduler can interleave it: the MFMAs
-    // of the next block's scores (from tile kt) run while the current scores become P (exp,
-    // row sum, rounding to T), then O^T += V^T P^T from V tile vt.
-    auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
-                    const unsigned char* vt) {
-        scores(kt, s_next);
-        const float m_use = (m == -INFINITY) ? 0.0f : m;
-        float sum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = fast_exp2(fmaf(s[t][r], cs, -m_use));
-                s[t][r] = e;
-                sum += e;
-            }
-        }
-        l += sum;
-        frag p[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = j >> 1;
-            const int h = j & 1;
-            p[j] = pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2], s[t][8 * h + 3],
-                                s[t][8 * h + 4], s[t][8 * h + 5], s[t][8 * h + 6],
-                                s[t][8 * h + 7]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const unsigned char* a0 = vt + v_off + 4 * j * GRP + dt * 256;
-                o[dt] = Elem<T>::mma(tr_frag_at<T>(a0, a0 + 2 * GRP), p[j], o[dt]);
-            }
-        }
-        // Interleave the score MFMAs with the softmax VALU work: a few K reads ahead, then per
-        // MFMA one more K read and about seven VALU ops; the P V MFMAs and their V reads follow.
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-        }
+    // Operand fragment i of the score MFMAs (K rows of tile half i / 8, k-step i % 8) and of
+    // the P V MFMAs (V^T for key group i / 4 and d tile i % 4).
+    auto k_frag = [&](const unsigned char* kt, int i) {
+        return as_frag<T>(ld16(kt + k_off + 8 * (i >> 3) * GRP + (i & 7) * 128));
+    };
+    auto v_frag = [&](const unsigned char* vt, int i) {
+        const unsigned char* a0 = vt + v_off + 4 * (i >> 2) * GRP + (i & 3) * 256;
+        return tr_frag_at<T>(a0, a0 + 2 * GRP);
     };
 
     // Blocks that need masking: keys past N, and with a causal mask the blocks that reach past
     // this wave's first row.
     auto needs_mask = [&](int key0) { return key0 + BN > N || (causal && key0 + BN - 1 > q0); };
 
+    // Exponential of score r of tile t, and the rounding of tile t's group h of eight scores
+    // to T (the P operand of key group 2 t + h).
+    auto exp_one = [&](f32x16 (&s)[2], int t, int r, float m_use) {
+        s[t][r] = fast_exp2(fmaf(s[t][r], cs, -m_use));
+    };
+    auto pack_p = [&](f32x16 (&s)[2], int t, int h) {
+        u32x4 pw = __builtin_bit_cast(
+            u32x4, pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2],
+                                s[t][8 * h + 3], s[t][8 * h + 4], s[t][8 * h + 5],
+                                s[t][8 * h + 6], s[t][8 * h + 7]));
+        // Keep the exponentials where they are placed: left alone, the compiler sinks them
+        // to their first use past the branches in between.
+        asm volatile("" : "+v"(pw));
+        return __builtin_bit_cast(frag, pw);
+    };
+
+    // One block with an explicit instruction order (the scheduling fences keep it), so that
+    // each MFMA is followed by a few VALU ops that do not depend on it:
+    //   phase A: the 16 MFMAs of the next block's scores (K tile kt) into s_next, each with the
+    //            exponential of one score of the current tile 0 (P groups 0 and 1);
+    //   phase B: the 16 MFMAs of O^T += V^T P^T (V tile vt), the first eight with the
+    //            exponentials of two scores of tile 1 (P groups 2 and 3, first used by MFMA 8),
+    //            each with the row sum of one packed pair of P and the max of two scores of
+    //            s_next.
+    // This splits the VALU work about evenly between the phases (the two waves of a SIMD run
+    // the same phase at the same time). The row sum is taken over P as rounded to T, the
+    // weights that P V applies. The next block's mask is applied between the phases. Every
+    // operand is read kAhead MFMAs before its product; the first V operands are read under the
+    // last score MFMAs. The tile loads of the iteration (K rows from kl_key0 into kl_dst if
+    // kl_do, V rows from vl_key0 into vl_dst if vl_do) are spread over the score MFMAs: issued
+    // together, the loads of all waves of a CU queue up behind each other and hold back the
+    // MFMAs. Returns this lane's raw row max of s_next.
+    auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
+                    const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
+                    unsigned char* kl_dst, bool vl_do, int vl_key0,
+                    unsigned char* vl_dst) -> float {
+        constexpr int kAhead = 3;
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        frag p[4];
+        frag fk[16];
+        frag fv[16];
+        s_next[0] = f32x16{};
+        s_next[1] = f32x16{};
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) fk[k] = k_frag(kt, k);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i + kAhead < 16) fk[i + kAhead] = k_frag(kt, i + kAhead);
+            else fv[i + kAhead - 16] = v_frag(vt, i + kAhead - 16);
+            s_next[i >> 3] = Elem<T>::mma(fk[i], qf[i & 7], s_next[i >> 3]);
+            // Load slots: every other MFMA, K parts in the first half, V parts in the second.
+            constexpr int kEvery = 4 / kParts;
+            const int slot = (i >> 1) & 3;
+            if ((i & 1) && slot % kEvery == kEvery - 1) {
+                if (i < 8 && kl_do) load_part(Kh, kl_key0, kl_dst, slot / kEvery);
+                if (i >= 8 && vl_do) load_part(Vh, vl_key0, vl_dst, slot / kEvery);
+            }
+            exp_one(s, 0, i, m_use);
+            if ((i & 7) == 7) p[i >> 3] = pack_p(s, 0, i >> 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
+        float mx = -INFINITY;
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i + kAhead < 16) fv[i + kAhead] = v_frag(vt, i + kAhead);
+            o[i & 3] = Elem<T>::mma(fv[i], p[i >> 2], o[i & 3]);
+            if (i < 8) {
+                exp_one(s, 1, 2 * i, m_use);
+                exp_one(s, 1, 2 * i + 1, m_use);
+                if ((i & 3) == 3) p[2 + (i >> 2)] = pack_p(s, 1, i >> 2);
+            }
+            sum = Elem<T>::sum2(__builtin_bit_cast(u32x4, p[i >> 2])[i & 3], sum);
+            const int t = i >> 3;
+            const int r = 2 * (i & 7);
+            mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, s_next[t][r]),
+                                               s_next[t][r + 1]);
+            // Keep both chains here: left alone, the compiler sinks them to their first use.
+            asm volatile("" : "+v"(sum), "+v"(mx));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l += sum;
+        return mx;
+    };
+
     // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
     // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
     // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
-    // buffers. Each iteration also forms the scores of block j+1 (for the last block they are
-    // formed from a stale buffer and discarded, which keeps the step free of branches). The
-    // loop is unrolled by two so that every buffer is a distinct LDS object.
+    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and their row max (for the
+    // last block they come from a stale buffer and the max is replaced by -inf, which leaves
+    // (m, l) unchanged). The loop is unrolled by two so that every buffer is a distinct LDS
+    // object.
     load_tile(Kh, 0, Kb0);
     load_tile(Vh, 0, Vb0);
     if (nkb > 1) load_tile(Kh, BN, Kb1);
@@ -384,30 +447,36 @@ __global__ void __launch_bounds__(256, 2)
     f32x16 sa[2], sb[2];
     float alpha;
     scores(Kb0, sa);
+    if (needs_mask(0)) mask_scores(sa, 0);
+    {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
+        }
+        update_max(mx, alpha);  // O is still zero: nothing to rescale
+    }
     for (int j = 0; j < nkb; j += 2) {
         // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (j + 2 < nkb) load_tile(Kh, (j + 2) * BN, Kb0);
-        if (j + 1 < nkb) load_tile(Vh, (j + 1) * BN, Vb1);
-        if (needs_mask(j * BN)) mask_scores(sa, j * BN);
-        if (update_max(sa, alpha)) {
+        float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                        j + 1 < nkb, (j + 1) * BN, Vb1);
+        if (update_max(j + 1 < nkb ? mx : -INFINITY, alpha)) {
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
         }
-        step(sa, Kb1, sb, Vb0);
         if (j + 1 >= nkb) break;
         // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (j + 3 < nkb) load_tile(Kh, (j + 3) * BN, Kb1);
-        if (j + 2 < nkb) load_tile(Vh, (j + 2) * BN, Vb0);
-        if (needs_mask((j + 1) * BN)) mask_scores(sb, (j + 1) * BN);
-        if (update_max(sb, alpha)) {
+        mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
+                  j + 2 < nkb, (j + 2) * BN, Vb0);
+        if (update_max(j + 2 < nkb ? mx : -INFINITY, alpha)) {
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
         }
-        step(sb, Kb0, sa, Vb1);
     }
 
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
@@ -589,13 +658,15 @@ template <typename T, int D>
 FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, float* L, int BH,
                                   int N, float scale, bool causal, hipStream_t stream) {
     using Cfg = dev::Fwd16Cfg<D>;
-    const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
+    constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
+    constexpr int BM = D == 128 ? 32 * kWaves128 : Cfg::BM;
+    const int nqb = (N + BM - 1) / BM;
     const long long blocks = static_cast<long long>(nqb) * BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int tok = profile_kernel<T, D>("forward", stream);
     if constexpr (D == 128) {
-        hipLaunchKernelGGL((dev::fwd16_d128_kernel<T>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+        hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0, stream, reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
                            L, N, nqb, scale * dev::kLog2e, causal ? 1 : 0);
