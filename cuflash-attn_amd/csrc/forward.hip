@@ -368,11 +368,11 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     //            exponential of one score of the current tile 0 (P groups 0 and 1);
     //   phase B: the 16 MFMAs of O^T += V^T P^T (V tile vt), the first eight with the
     //            exponentials of two scores of tile 1 (P groups 2 and 3, first used by MFMA 8),
-    //            each with the row sum of one packed pair of P and the max of two scores of
-    //            s_next.
+    //            each with two terms of the row sum and the max of two scores of s_next.
     // This splits the VALU work about evenly between the phases (the two waves of a SIMD run
-    // the same phase at the same time). The row sum is taken over P as rounded to T, the
-    // weights that P V applies. The next block's mask is applied between the phases. Every
+    // the same phase at the same time). The row sum is taken over the fp32 exponentials, before
+    // their rounding to T for P V, as in the reference. The next block's mask is applied
+    // between the phases. Every
     // operand is read kAhead MFMAs before its product; the first V operands are read under the
     // last score MFMAs. The tile loads of the iteration (K rows from kl_key0 into kl_dst if
     // kl_do, V rows from vl_key0 into vl_dst if vl_do) are spread over the score MFMAs: issued
@@ -419,7 +419,8 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                 exp_one(s, 1, 2 * i + 1, m_use);
                 if ((i & 3) == 3) p[2 + (i >> 2)] = pack_p(s, 1, i >> 2);
             }
-            sum = Elem<T>::sum2(__builtin_bit_cast(u32x4, p[i >> 2])[i & 3], sum);
+            // Row sum of the fp32 exponentials (tile 0 in MFMAs 0-7, tile 1 in MFMAs 8-15).
+            sum += s[i >> 3][2 * (i & 7)] + s[i >> 3][2 * (i & 7) + 1];
             const int t = i >> 3;
             const int r = 2 * (i & 7);
             mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, s_next[t][r]),
