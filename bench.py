@@ -106,6 +106,8 @@ def parse():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg3", "decode", "copy"), default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
+    ap.add_argument("--cpu-seq", type=int, default=2048,
+                    help="sequence length of the CPU baseline sample (default 2048)")
     ap.add_argument("--cpu-heads", type=int, default=0,
                     help="heads in the CPU-baseline sample (default: one per host thread, <= 16)")
     return ap.parse_args()
@@ -308,19 +310,22 @@ def main():
 
         threads = host_threads()
         heads = args.cpu_heads or threads
-        log(f"CPU baseline: naive fp32 fwd+bwd on {heads} heads, {threads} threads")
-        sample = (1, heads, N, D)
+        ncpu = args.cpu_seq
+        log(f"CPU baseline: naive fp32 fwd+bwd on {heads} heads of N={ncpu}, {threads} threads")
+        sample = (1, heads, ncpu, D)
         xs = [synth.normal(s, sample) for s in (1, 2, 3, 4)]
         c0 = time.perf_counter()
         oracle.naive_forward_f32(xs[0], xs[1], xs[2], scale, causal, nthreads=threads)
         oracle.naive_backward_f32(xs[0], xs[1], xs[2], xs[3], scale, causal, nthreads=threads)
         secs = time.perf_counter() - c0
-        f_sample = flops_fwd(1, heads, N, D, causal) * 3.5
+        f_sample = flops_fwd(1, heads, ncpu, D, causal) * 3.5
         cpu = {"value": round(f_sample / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
                "kind": "port", "seconds": round(secs, 2),
-               "sample": f"config-3 shape with B=1 H={heads} (of B*H=32 heads), fwd+bwd, naive "
-                         f"O(N^2) fp32 (reference test_forward.cu:21-118 / test_backward.cu:"
-                         f"21-127 restated in C), one thread per head, same FLOP model"}
+               "sample": f"config-3 head shape with N={ncpu} (config 3: {N}; the naive loops "
+                         f"parallelize over heads only, so N bounds the time), B=1 H={heads}, "
+                         f"fwd+bwd, naive O(N^2) fp32 (reference test_forward.cu:21-118 / "
+                         f"test_backward.cu:21-127 restated in C), one thread per head, same "
+                         f"FLOP model"}
 
     out = {
         "metric": "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM GB/s at 32k KV",
