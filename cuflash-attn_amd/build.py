@@ -24,7 +24,11 @@ BUILD_DIR = os.path.join(REPO_ROOT, "build")
 LIB_NAME = "libcuflash_attn.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
 
-SOURCES = ["api.cpp", "profile.cpp", "forward.hip", "backward.hip", "decode.hip"]
+SOURCES = ["api.cpp", "profile.cpp", "forward.hip", "backward.hip", "decode.hip",
+           "primitives.hip"]
+# C++ test programs linked against the library (sources under tests/cpp, binaries in build/).
+TEST_PROGRAMS = {"test_primitives": "test_primitives.cpp"}
+TEST_SRC = os.path.join(REPO_ROOT, "tests", "cpp")
 
 # Packed-FP32 VALU forms are disabled for all device code (v_pk_{add,mul,fma}_f32).
 COMMON_FLAGS = [
@@ -72,6 +76,17 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    for name, src in TEST_PROGRAMS.items():
+        out = os.path.join(BUILD_DIR, name)
+        cmd = [hipcc(), "-x", "hip", "--offload-arch=gfx950", "-O2", "-std=c++17",
+               "-I" + INCLUDE, os.path.join(TEST_SRC, src), "-x", "none", LIB_PATH,
+               "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")
+        os.replace(out + ".tmp", out)
+        if verbose:
+            print(f"built {out}")
     return LIB_PATH
 
 

@@ -157,3 +157,64 @@ def test_candidate_paths_follow_reference_order(monkeypatch):
 def test_missing_library_fails_loudly():
     with pytest.raises(OSError):
         cuflash_attn.load_library("/nonexistent/libcuflash_attn.so")
+
+
+# The primitive layer cuflash::kernels::* (include/cuflash/kernels/*.cuh): every instantiation the
+# reference library exports (src/kernels/matmul.cu:236-319, tile_io.cu:229-287,
+# online_softmax.cu:160-246) must be exported, with the HIP stream type.
+MATMUL_SHAPES = [(64, 64, 32), (32, 32, 32), (64, 64, 64), (32, 32, 128), (64, 64, 128),
+                 (32, 64, 32), (32, 64, 64), (64, 32, 64)]
+TILE_SHAPES = [(64, 64), (64, 32), (32, 32), (32, 64), (32, 128), (64, 128)]
+
+
+def _primitive_signatures():
+    f, s = "ihipStream_t*", "int, int, int, int, int"
+    sigs = []
+    for m, n, k in MATMUL_SHAPES:
+        for op in ("matmul_ABt", "matmul_AB", "matmul_AB_acc", "matmul_AtB"):
+            sigs.append(f"cuflash::kernels::{op}<{m}, {n}, {k}>(float const*, float const*, "
+                        f"float*, float, {f})")
+    for r, c in TILE_SHAPES:
+        sigs += [f"cuflash::kernels::load_tile<{r}, {c}>(float const*, float*, {s}, {f})",
+                 f"cuflash::kernels::load_tile<{r}, {c}>(__half const*, float*, {s}, {f})",
+                 f"cuflash::kernels::store_tile<{r}, {c}>(float const*, float*, {s}, {f})",
+                 f"cuflash::kernels::store_tile<{r}, {c}>(float const*, __half*, {s}, {f})"]
+    sigs.append(f"cuflash::kernels::load_store_tile_roundtrip<64, 64>(float const*, float*, {s}, "
+                f"{f})")
+    sigs += [f"cuflash::kernels::online_softmax_init(float*, float*, int, {f})",
+             f"cuflash::kernels::online_softmax_update(float const*, float const*, float*, "
+             f"float*, int, {f})",
+             f"cuflash::kernels::online_softmax_finalize(float const*, float const*, float*, "
+             f"float*, int, {f})",
+             f"cuflash::kernels::online_softmax_forward(float const*, float*, float*, int, int, "
+             f"int, {f})"]
+    return sigs
+
+
+def test_primitive_layer_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", lib.path], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set()
+    for line in out.splitlines():
+        parts = line.split(" ", 2)
+        if len(parts) == 3 and parts[1] in ("T", "W"):
+            exported.add(parts[2].replace("cuflash::FlashAttentionError ", ""))
+    sigs = _primitive_signatures()
+    assert len(sigs) == 61
+    missing = [s for s in sigs if s not in exported]
+    assert not missing, missing
+
+
+def test_primitive_headers_declare_the_reference_api():
+    """Every primitive the reference declares (include/cuflash/kernels/*.cuh) is declared here
+    under the same name and header file name."""
+    names = {"matmul.cuh": ["matmul_ABt", "matmul_AB", "matmul_AB_acc", "matmul_AtB"],
+             "online_softmax.cuh": ["online_softmax_init", "online_softmax_update",
+                                    "online_softmax_finalize", "online_softmax_forward",
+                                    "warp_reduce_max", "warp_reduce_sum"],
+             "tile_io.cuh": ["load_tile", "store_tile", "load_store_tile_roundtrip"]}
+    for header, fns in names.items():
+        text = open(os.path.join(REPO, "include", "cuflash", "kernels", header)).read()
+        assert "namespace kernels" in text
+        for fn in fns:
+            assert re.search(r"\b" + fn + r"\(", text), (header, fn)
