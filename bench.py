@@ -303,6 +303,69 @@ def main():
                                "traffic": committed_traffic(f"decode_split_f16_d{Dd}")}}
         del kd, vd
 
+        # Decode extensions at the config-4 size: grouped-query heads (32 query heads over 8
+        # key/value heads, so each K/V row serves 4 query heads) and the same keys in a paged
+        # cache (16-key pages in shuffled order). Reported beside the headline, not in `value`.
+        Hkv, page = 8, 16
+        torch.cuda.empty_cache()
+        g.manual_seed(4)
+        kg = torch.randn((Bd, Hkv, LKV, Dd), generator=g, device=dev, dtype=torch.float16)
+        g.manual_seed(5)
+        vg = torch.randn((Bd, Hkv, LKV, Dd), generator=g, device=dev, dtype=torch.float16)
+        ext_bytes = Bd * Hkv * LKV * Dd * 2 * 2 + Bd * Hd * Dd * 2 * 2 + Bd * Hd * 4
+
+        def time_ext(fn, label):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            lib.profile_enable(True)
+            t0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            rep = lib.profile_report()
+            lib.profile_enable(False)
+            ms = t0.elapsed_time(t1) / args.steps
+            sk = rep.get(f"decode_split_f16_d{Dd}", (1, float("nan")))
+            return {"ms": round(ms, 4), "GB/s": round(ext_bytes / (ms * 1e-3) / 1e9, 1),
+                    "split_kernel_ms": round(sk[1] / sk[0], 4),
+                    "frac_of_hbm": round(ext_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "alg_bytes": ext_bytes, "workload": label}
+
+        gqa = lib.fn("decode_gqa", "f16")
+
+        def run_gqa():
+            st = gqa(qd.data_ptr(), kg.data_ptr(), vg.data_ptr(), od.data_ptr(), ld.data_ptr(),
+                     Bd, Hd, Hkv, LKV, Dd, Dd ** -0.5, 0, sp)
+            if st != 0:
+                raise RuntimeError(f"decode_gqa status {st}")
+        ext = {"gqa": time_ext(run_gqa, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}")}
+
+        npages = Bd * LKV // page
+        kp = kg.reshape(Bd, Hkv, LKV // page, page, Dd).permute(0, 2, 3, 1, 4).reshape(
+            npages, page, Hkv, Dd)
+        vp = vg.reshape(Bd, Hkv, LKV // page, page, Dd).permute(0, 2, 3, 1, 4).reshape(
+            npages, page, Hkv, Dd)
+        del kg, vg
+        perm = torch.randperm(npages, generator=g, device=dev)
+        kp = kp[perm].contiguous()
+        vp = vp[perm].contiguous()
+        table = torch.argsort(perm).to(torch.int32).reshape(Bd, LKV // page).contiguous()
+        lens = torch.full((Bd,), LKV, dtype=torch.int32, device=dev)
+        paged = lib.fn("decode_paged", "f16")
+
+        def run_paged():
+            st = paged(qd.data_ptr(), kp.data_ptr(), vp.data_ptr(), od.data_ptr(), ld.data_ptr(),
+                       table.data_ptr(), lens.data_ptr(), Bd, Hd, Hkv, page, LKV // page, Dd,
+                       Dd ** -0.5, 0, sp)
+            if st != 0:
+                raise RuntimeError(f"decode_paged status {st}")
+        ext["paged"] = time_ext(run_paged, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}, "
+                                           f"{page}-key pages in shuffled order")
+        decode["extensions"] = ext
+        del kp, vp, table, lens, perm
+
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
     if not args.no_cpu_baseline:

@@ -78,6 +78,37 @@ FlashAttentionError check_decode(const void* Q, const void* K, const void* V, co
     return FlashAttentionError::SUCCESS;
 }
 
+// Grouped-query decode: the decode checks with the key/value head count, then the grouping
+// (num_heads a multiple of num_kv_heads, else DIMENSION_MISMATCH).
+FlashAttentionError check_decode_gqa(const void* Q, const void* K, const void* V, const void* O,
+                                     const void* L, int batch_size, int num_heads,
+                                     int num_kv_heads, int kv_len, int head_dim, float scale,
+                                     int num_splits) {
+    FlashAttentionError err =
+        check_decode(Q, K, V, O, L, batch_size, num_heads, kv_len, head_dim, scale, num_splits);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    if (num_kv_heads <= 0) return FlashAttentionError::INVALID_DIMENSION;
+    if (num_heads % num_kv_heads != 0) return FlashAttentionError::DIMENSION_MISMATCH;
+    return FlashAttentionError::SUCCESS;
+}
+
+// Paged decode: every pointer (also block_table and seq_lens) non-null, then page_size and
+// max_pages_per_seq positive; the capacity page_size * max_pages_per_seq then stands in for
+// kv_len in the grouped-query checks.
+FlashAttentionError check_decode_paged(const void* Q, const void* K, const void* V,
+                                       const void* O, const void* L, const int* block_table,
+                                       const int* seq_lens, int batch_size, int num_heads,
+                                       int num_kv_heads, int page_size, int max_pages_per_seq,
+                                       int head_dim, float scale, int num_splits) {
+    if (!Q || !K || !V || !O || !L || !block_table || !seq_lens)
+        return FlashAttentionError::NULL_POINTER;
+    if (page_size <= 0 || max_pages_per_seq <= 0) return FlashAttentionError::INVALID_DIMENSION;
+    const long long cap = static_cast<long long>(page_size) * max_pages_per_seq;
+    if (cap > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    return check_decode_gqa(Q, K, V, O, L, batch_size, num_heads, num_kv_heads,
+                            static_cast<int>(cap), head_dim, scale, num_splits);
+}
+
 template <typename T>
 FlashAttentionError forward_impl(const T* Q, const T* K, const T* V, T* O, float* L, int b,
                                  int h, int n, int d, float scale, bool causal,
@@ -104,6 +135,29 @@ FlashAttentionError decode_impl(const T* Q, const T* K, const T* V, T* O, float*
     FlashAttentionError err = check_decode(Q, K, V, O, L, b, h, kv_len, d, scale, num_splits);
     if (err != FlashAttentionError::SUCCESS) return err;
     return detail::launch_decode<T>(Q, K, V, O, L, b, h, kv_len, d, scale, num_splits, stream);
+}
+
+template <typename T>
+FlashAttentionError decode_gqa_impl(const T* Q, const T* K, const T* V, T* O, float* L, int b,
+                                    int h, int hkv, int kv_len, int d, float scale,
+                                    int num_splits, hipStream_t stream) {
+    FlashAttentionError err =
+        check_decode_gqa(Q, K, V, O, L, b, h, hkv, kv_len, d, scale, num_splits);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    return detail::launch_decode_gqa<T>(Q, K, V, O, L, b, h, hkv, kv_len, d, scale, num_splits,
+                                        stream);
+}
+
+template <typename T>
+FlashAttentionError decode_paged_impl(const T* Q, const T* Kc, const T* Vc, T* O, float* L,
+                                      const int* table, const int* lens, int b, int h, int hkv,
+                                      int page_size, int max_pages, int d, float scale,
+                                      int num_splits, hipStream_t stream) {
+    FlashAttentionError err = check_decode_paged(Q, Kc, Vc, O, L, table, lens, b, h, hkv,
+                                                 page_size, max_pages, d, scale, num_splits);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    return detail::launch_decode_paged<T>(Q, Kc, Vc, O, L, table, lens, b, h, hkv, page_size,
+                                          max_pages, d, scale, num_splits, stream);
 }
 
 }  // namespace
@@ -188,6 +242,66 @@ FlashAttentionError flash_attention_decode(const __hip_bfloat16* Q, const __hip_
                        stream);
 }
 
+FlashAttentionError flash_attention_decode_gqa(const float* Q, const float* K, const float* V,
+                                               float* O, float* L, int batch_size, int num_heads,
+                                               int num_kv_heads, int kv_len, int head_dim,
+                                               float scale, int num_splits, hipStream_t stream) {
+    return decode_gqa_impl(Q, K, V, O, L, batch_size, num_heads, num_kv_heads, kv_len, head_dim,
+                           scale, num_splits, stream);
+}
+
+FlashAttentionError flash_attention_decode_paged(const float* Q, const float* K_cache,
+                                                 const float* V_cache, float* O, float* L,
+                                                 const int* block_table, const int* seq_lens,
+                                                 int batch_size, int num_heads, int num_kv_heads,
+                                                 int page_size, int max_pages_per_seq,
+                                                 int head_dim, float scale, int num_splits,
+                                                 hipStream_t stream) {
+    return decode_paged_impl(Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size,
+                             num_heads, num_kv_heads, page_size, max_pages_per_seq, head_dim,
+                             scale, num_splits, stream);
+}
+
+FlashAttentionError flash_attention_decode_gqa(const __half* Q, const __half* K, const __half* V,
+                                               __half* O, float* L, int batch_size, int num_heads,
+                                               int num_kv_heads, int kv_len, int head_dim,
+                                               float scale, int num_splits, hipStream_t stream) {
+    return decode_gqa_impl(Q, K, V, O, L, batch_size, num_heads, num_kv_heads, kv_len, head_dim,
+                           scale, num_splits, stream);
+}
+
+FlashAttentionError flash_attention_decode_paged(const __half* Q, const __half* K_cache,
+                                                 const __half* V_cache, __half* O, float* L,
+                                                 const int* block_table, const int* seq_lens,
+                                                 int batch_size, int num_heads, int num_kv_heads,
+                                                 int page_size, int max_pages_per_seq,
+                                                 int head_dim, float scale, int num_splits,
+                                                 hipStream_t stream) {
+    return decode_paged_impl(Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size,
+                             num_heads, num_kv_heads, page_size, max_pages_per_seq, head_dim,
+                             scale, num_splits, stream);
+}
+
+FlashAttentionError flash_attention_decode_gqa(const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+                                               __hip_bfloat16* O, float* L, int batch_size, int num_heads,
+                                               int num_kv_heads, int kv_len, int head_dim,
+                                               float scale, int num_splits, hipStream_t stream) {
+    return decode_gqa_impl(Q, K, V, O, L, batch_size, num_heads, num_kv_heads, kv_len, head_dim,
+                           scale, num_splits, stream);
+}
+
+FlashAttentionError flash_attention_decode_paged(const __hip_bfloat16* Q, const __hip_bfloat16* K_cache,
+                                                 const __hip_bfloat16* V_cache, __hip_bfloat16* O, float* L,
+                                                 const int* block_table, const int* seq_lens,
+                                                 int batch_size, int num_heads, int num_kv_heads,
+                                                 int page_size, int max_pages_per_seq,
+                                                 int head_dim, float scale, int num_splits,
+                                                 hipStream_t stream) {
+    return decode_paged_impl(Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size,
+                             num_heads, num_kv_heads, page_size, max_pages_per_seq, head_dim,
+                             scale, num_splits, stream);
+}
+
 }  // namespace cuflash
 
 // ===== C ABI (reference src/api/flash_attention_api.cu:186-242) =====
@@ -270,6 +384,69 @@ int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const __hip_bfloat16*
                                   float scale, int num_splits, hipStream_t stream) {
     return static_cast<int>(cuflash::flash_attention_decode(
         Q, K, V, O, L, batch_size, num_heads, kv_len, head_dim, scale, num_splits, stream));
+}
+
+int cuflash_attention_decode_gqa_f32(const float* Q, const float* K, const float* V, float* O,
+                                     float* L, int batch_size, int num_heads, int num_kv_heads,
+                                     int kv_len, int head_dim, float scale, int num_splits,
+                                     hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_gqa(Q, K, V, O, L, batch_size,
+                                                                num_heads, num_kv_heads, kv_len,
+                                                                head_dim, scale, num_splits,
+                                                                stream));
+}
+
+int cuflash_attention_decode_paged_f32(const float* Q, const float* K_cache, const float* V_cache,
+                                       float* O, float* L, const int* block_table,
+                                       const int* seq_lens, int batch_size, int num_heads,
+                                       int num_kv_heads, int page_size, int max_pages_per_seq,
+                                       int head_dim, float scale, int num_splits,
+                                       hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_paged(
+        Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size, num_heads, num_kv_heads,
+        page_size, max_pages_per_seq, head_dim, scale, num_splits, stream));
+}
+
+int cuflash_attention_decode_gqa_f16(const __half* Q, const __half* K, const __half* V, __half* O,
+                                     float* L, int batch_size, int num_heads, int num_kv_heads,
+                                     int kv_len, int head_dim, float scale, int num_splits,
+                                     hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_gqa(Q, K, V, O, L, batch_size,
+                                                                num_heads, num_kv_heads, kv_len,
+                                                                head_dim, scale, num_splits,
+                                                                stream));
+}
+
+int cuflash_attention_decode_paged_f16(const __half* Q, const __half* K_cache, const __half* V_cache,
+                                       __half* O, float* L, const int* block_table,
+                                       const int* seq_lens, int batch_size, int num_heads,
+                                       int num_kv_heads, int page_size, int max_pages_per_seq,
+                                       int head_dim, float scale, int num_splits,
+                                       hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_paged(
+        Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size, num_heads, num_kv_heads,
+        page_size, max_pages_per_seq, head_dim, scale, num_splits, stream));
+}
+
+int cuflash_attention_decode_gqa_bf16(const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V, __hip_bfloat16* O,
+                                     float* L, int batch_size, int num_heads, int num_kv_heads,
+                                     int kv_len, int head_dim, float scale, int num_splits,
+                                     hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_gqa(Q, K, V, O, L, batch_size,
+                                                                num_heads, num_kv_heads, kv_len,
+                                                                head_dim, scale, num_splits,
+                                                                stream));
+}
+
+int cuflash_attention_decode_paged_bf16(const __hip_bfloat16* Q, const __hip_bfloat16* K_cache, const __hip_bfloat16* V_cache,
+                                       __hip_bfloat16* O, float* L, const int* block_table,
+                                       const int* seq_lens, int batch_size, int num_heads,
+                                       int num_kv_heads, int page_size, int max_pages_per_seq,
+                                       int head_dim, float scale, int num_splits,
+                                       hipStream_t stream) {
+    return static_cast<int>(cuflash::flash_attention_decode_paged(
+        Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size, num_heads, num_kv_heads,
+        page_size, max_pages_per_seq, head_dim, scale, num_splits, stream));
 }
 
 const char* cuflash_version(void) { return CUFLASH_VERSION; }

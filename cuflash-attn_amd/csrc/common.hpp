@@ -58,11 +58,11 @@ struct Elem<__hip_bfloat16> {
     static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
-    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_bf16 with (1, 1)).
-    static __device__ __forceinline__ float sum2(uint32_t v, float acc) {
+    // acc + a.lo b.lo + a.hi b.hi of two packed pairs, in fp32 (v_dot2_f32_bf16).
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
         typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v),
-                                               __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                               __builtin_bit_cast(bf16x2, b), acc, false);
     }
 };
 
@@ -80,11 +80,11 @@ struct Elem<__half> {
     static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
-    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_f16 with (1, 1)).
-    static __device__ __forceinline__ float sum2(uint32_t v, float acc) {
+    // acc + a.lo b.lo + a.hi b.hi of two packed pairs, in fp32 (v_dot2_f32_f16).
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
         typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, v),
-                                      __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b),
+                                      acc, false);
     }
 };
 

@@ -80,44 +80,112 @@ __device__ __forceinline__ float exp2_rel(float x, float m) {
     return x == -INFINITY ? 0.0f : fast_exp2(x - m);
 }
 
-template <typename T, int D>
+// Where the keys come from. Contiguous: K, V [B, Hkv, kv_len, D]. Paged: K, V
+// [num_pages, page_size, Hkv, D] with block_table [B, max_pages] naming the page of each
+// page_size keys of a sequence and seq_lens [B] its length (clamped to [0, kv_len], kv_len =
+// max_pages * page_size). A workgroup serves G query heads that share one key/value head:
+// query head h reads key/value head h / (H / Hkv).
+struct DecodeArgs {
+    const int* block_table;
+    const int* seq_lens;
+    int H, Hkv;
+    int kv_len;
+    int page_size, max_pages;
+    int page_shift;  // log2(page_size) when it is a power of two, else -1
+    int chunk, nsplit;
+    float c;  // scale * log2(e)
+};
+
+template <typename T, int D, int G, bool PAGED>
 __global__ void __launch_bounds__(256)
     decode_split_kernel(const typename Mma<T>::elem* __restrict__ Q,
                         const typename Mma<T>::elem* __restrict__ K,
                         const typename Mma<T>::elem* __restrict__ V, float* __restrict__ part_acc,
-                        float2* __restrict__ part_ml, int kv_len, int chunk, int nsplit, float c) {
+                        float2* __restrict__ part_ml, DecodeArgs a) {
     using Cfg = DecCfg<T, D>;
     constexpr int VEC = Cfg::VEC;
     constexpr int LPR = Cfg::LPR;
     constexpr int RPW = Cfg::RPW;
-    constexpr int U = Cfg::UNROLL;
+    // Rows in flight per lane group: fewer when the workgroup carries several query heads.
+    constexpr int U = G <= 2 ? Cfg::UNROLL : Cfg::UNROLL / 2;
+    constexpr int ROWS_PER_ITER = RPW * U * Cfg::kWaves;
 
-    const int bh = blockIdx.x / nsplit;
-    const int split = blockIdx.x % nsplit;
+    // blockIdx.x = ((b * Hkv + hk) * NG + g) * nsplit + split, NG = (H / Hkv) / G.
+    const int hpk = a.H / a.Hkv;
+    const int NG = hpk / G;
+    int rest = blockIdx.x;
+    const int split = rest % a.nsplit;
+    rest /= a.nsplit;
+    const int g = rest % NG;
+    rest /= NG;
+    const int hk = rest % a.Hkv;
+    const int b = rest / a.Hkv;
+    const int h0 = hk * hpk + g * G;  // first query head of the workgroup
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int grp = lane / LPR;   // row slot inside a wave load
     const int part = lane % LPR;  // which 16-byte chunk of the row
 
-    const size_t head = static_cast<size_t>(bh) * kv_len * D;
-    const int kbeg = split * chunk;
-    const int kend = min(kv_len, kbeg + chunk);
+    const int kv_b = PAGED ? min(max(a.seq_lens[b], 0), a.kv_len) : a.kv_len;
+    const int kbeg = split * a.chunk;
+    const int kend = min(kv_b, kbeg + a.chunk);
 
-    float qv[VEC];
-    to_floats<T, VEC>(ld16(Q + static_cast<size_t>(bh) * D + part * VEC), qv);
+    // Page of key row t and the row's offset inside it (paged cache).
+    auto page_of = [&](int t) {
+        const int j = a.page_shift >= 0 ? t >> a.page_shift : t / a.page_size;
+        return a.block_table[static_cast<size_t>(b) * a.max_pages + j];
+    };
+    auto in_page = [&](int t) {
+        return a.page_shift >= 0 ? t & (a.page_size - 1) : t % a.page_size;
+    };
+    // Element offset of key row t of this (batch, key/value head); `page` is page_of(t).
+    auto row_off = [&](int t, int page) -> size_t {
+        if constexpr (PAGED) {
+            return ((static_cast<size_t>(page) * a.page_size + in_page(t)) * a.Hkv + hk) * D;
+        } else {
+            return (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D +
+                   static_cast<size_t>(t) * D;
+        }
+    };
+
+    // Q: 16-bit types keep the row chunk packed for v_dot2 (the scale is applied to the dot
+    // product); fp32 holds it pre-scaled.
+    constexpr bool kPacked = !std::is_same<T, float>::value;
+    u32x4 qp[G];
+    float qv[G][VEC];
+    float m[G], l[G];
+    float acc[G][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) qv[i] *= c;  // scores come out in log2 units
-
-    float m = -INFINITY;
-    float l = 0.0f;
-    float acc[VEC];
+    for (int gi = 0; gi < G; ++gi) {
+        const size_t qrow = static_cast<size_t>(b) * a.H + h0 + gi;
+        qp[gi] = ld16(Q + qrow * D + part * VEC);
+        to_floats<T, VEC>(qp[gi], qv[gi]);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[i] = 0.0f;
+        for (int i = 0; i < VEC; ++i) {
+            qv[gi][i] *= a.c;  // scores come out in log2 units
+            acc[gi][i] = 0.0f;
+        }
+        m[gi] = -INFINITY;
+        l[gi] = 0.0f;
+    }
 
-    const typename Mma<T>::elem* Kh = K + head + part * VEC;
-    const typename Mma<T>::elem* Vh = V + head + part * VEC;
-    for (int base = kbeg + wave * RPW * U; base < kend; base += Cfg::ROWS_PER_ITER) {
+    const typename Mma<T>::elem* Kp = K + part * VEC;
+    const typename Mma<T>::elem* Vp = V + part * VEC;
+    // Paged: the page indices of an iteration's rows are fetched one iteration ahead, so their
+    // latency does not add to that of the K / V loads that depend on them.
+    int pg[U];
+    auto fetch_pages = [&](int bs) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int row = bs + u * RPW + grp;
+            pg[u] = (PAGED && row < kend) ? page_of(row) : 0;
+        }
+    };
+    const int first = kbeg + wave * RPW * U;
+    if constexpr (PAGED) fetch_pages(first);
+    for (int base = first; base < kend; base += ROWS_PER_ITER) {
         u32x4 kr[U], vr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -125,81 +193,102 @@ __global__ void __launch_bounds__(256)
             kr[u] = u32x4{0u, 0u, 0u, 0u};
             vr[u] = u32x4{0u, 0u, 0u, 0u};
             if (row < kend) {
-                kr[u] = ld16(Kh + static_cast<size_t>(row) * D);
-                vr[u] = ld16(Vh + static_cast<size_t>(row) * D);
+                const size_t off = row_off(row, pg[u]);
+                kr[u] = ld16(Kp + off);
+                vr[u] = ld16(Vp + off);
             }
         }
-        float s[U];
-        float mblk = -INFINITY;
+        if constexpr (PAGED) fetch_pages(base + ROWS_PER_ITER);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float kf[VEC];
-            to_floats<T, VEC>(kr[u], kf);
-            float dot = 0.0f;
+        for (int gi = 0; gi < G; ++gi) {
+            float s[U];
+            float mblk = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) dot = fmaf(qv[i], kf[i], dot);
-            dot = group_sum<LPR>(dot);
-            s[u] = (base + u * RPW + grp < kend) ? dot : -INFINITY;
-            mblk = fmaxf(mblk, s[u]);
+            for (int u = 0; u < U; ++u) {
+                float dot = 0.0f;
+                if constexpr (kPacked) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dot = Elem<T>::dot2(qp[gi][j], kr[u][j], dot);
+                    dot = group_sum<LPR>(dot) * a.c;
+                } else {
+                    float kf[VEC];
+                    to_floats<T, VEC>(kr[u], kf);
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) dot = fmaf(qv[gi][i], kf[i], dot);
+                    dot = group_sum<LPR>(dot);
+                }
+                s[u] = (base + u * RPW + grp < kend) ? dot : -INFINITY;
+                mblk = fmaxf(mblk, s[u]);
+            }
+            const float m_new = fmaxf(m[gi], mblk);
+            const float alpha = exp2_rel(m[gi], m_new);
+            l[gi] *= alpha;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) acc[gi][i] *= alpha;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float p = exp2_rel(s[u], m_new);
+                float vf[VEC];
+                to_floats<T, VEC>(vr[u], vf);
+                l[gi] += p;
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) acc[gi][i] = fmaf(p, vf[i], acc[gi][i]);
+            }
+            m[gi] = m_new;
         }
-        const float m_new = fmaxf(m, mblk);
-        const float alpha = exp2_rel(m, m_new);
-        l *= alpha;
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] *= alpha;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float p = exp2_rel(s[u], m_new);
-            float vf[VEC];
-            to_floats<T, VEC>(vr[u], vf);
-            l += p;
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) acc[i] = fmaf(p, vf[i], acc[i]);
-        }
-        m = m_new;
     }
 
     // Merge the RPW row slots of the wave (lanes part, part + LPR, ...).
 #pragma unroll
-    for (int w = LPR; w < 64; w <<= 1) {
-        const float m2 = xor_shuffle(m, w);
-        const float l2 = xor_shuffle(l, w);
-        const float mm = fmaxf(m, m2);
-        const float f1 = exp2_rel(m, mm);
-        const float f2 = exp2_rel(m2, mm);
-        l = l * f1 + l2 * f2;
+    for (int gi = 0; gi < G; ++gi) {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] = acc[i] * f1 + xor_shuffle(acc[i], w) * f2;
-        m = mm;
+        for (int w = LPR; w < 64; w <<= 1) {
+            const float m2 = xor_shuffle(m[gi], w);
+            const float l2 = xor_shuffle(l[gi], w);
+            const float mm = fmaxf(m[gi], m2);
+            const float f1 = exp2_rel(m[gi], mm);
+            const float f2 = exp2_rel(m2, mm);
+            l[gi] = l[gi] * f1 + l2 * f2;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i)
+                acc[gi][i] = acc[gi][i] * f1 + xor_shuffle(acc[gi][i], w) * f2;
+            m[gi] = mm;
+        }
     }
 
     // Merge the waves through LDS.
-    __shared__ float s_m[Cfg::kWaves];
-    __shared__ float s_l[Cfg::kWaves];
-    __shared__ __attribute__((aligned(16))) float s_acc[Cfg::kWaves][D];
+    __shared__ float s_m[Cfg::kWaves][G];
+    __shared__ float s_l[Cfg::kWaves][G];
+    __shared__ __attribute__((aligned(16))) float s_acc[Cfg::kWaves][G][D];
     if (lane < LPR) {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) s_acc[wave][part * VEC + i] = acc[i];
-        if (lane == 0) {
-            s_m[wave] = m;
-            s_l[wave] = l;
+        for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) s_acc[wave][gi][part * VEC + i] = acc[gi][i];
+            if (lane == 0) {
+                s_m[wave][gi] = m[gi];
+                s_l[wave][gi] = l[gi];
+            }
         }
     }
     __syncthreads();
     if (tid < D) {
-        float mm = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < Cfg::kWaves; ++w) mm = fmaxf(mm, s_m[w]);
-        float lt = 0.0f, at = 0.0f;
+        for (int gi = 0; gi < G; ++gi) {
+            float mm = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < Cfg::kWaves; ++w) {
-            const float f = exp2_rel(s_m[w], mm);
-            lt += s_l[w] * f;
-            at += s_acc[w][tid] * f;
+            for (int w = 0; w < Cfg::kWaves; ++w) mm = fmaxf(mm, s_m[w][gi]);
+            float lt = 0.0f, at = 0.0f;
+#pragma unroll
+            for (int w = 0; w < Cfg::kWaves; ++w) {
+                const float f = exp2_rel(s_m[w][gi], mm);
+                lt += s_l[w][gi] * f;
+                at += s_acc[w][gi][tid] * f;
+            }
+            const size_t slot = (static_cast<size_t>(b) * a.H + h0 + gi) * a.nsplit + split;
+            part_acc[slot * D + tid] = at;
+            if (tid == 0) part_ml[slot] = make_float2(mm, lt);
         }
-        const size_t slot = static_cast<size_t>(bh) * nsplit + split;
-        part_acc[slot * D + tid] = at;
-        if (tid == 0) part_ml[slot] = make_float2(mm, lt);
     }
 }
 
@@ -221,13 +310,14 @@ __global__ void __launch_bounds__(D)
         lt += v.y * f;
         at += acc[static_cast<size_t>(s) * D + d] * f;
     }
-    const float o = at / lt;
+    // lt == 0 only when every split was empty (a paged sequence of length 0): O = 0, L = -inf.
+    const float o = lt == 0.0f ? 0.0f : at / lt;
     if constexpr (std::is_same<T, float>::value) {
         O[static_cast<size_t>(bh) * D + d] = o;
     } else {
         O[static_cast<size_t>(bh) * D + d] = static_cast<uint16_t>(Elem<T>::pack2(o, 0.0f) & 0xffffu);
     }
-    if (d == 0) L[bh] = (mm + fast_log2(lt)) * kLn2;
+    if (d == 0) L[bh] = lt == 0.0f ? -INFINITY : (mm + fast_log2(lt)) * kLn2;
 }
 
 }  // namespace dev
@@ -256,18 +346,25 @@ int choose_splits(int requested, int BH, int kv_len) {
     return std::max(1, std::min(s, max_useful));
 }
 
-template <typename T, int D>
-FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* L, int BH,
-                               int kv_len, float scale, int num_splits, hipStream_t stream) {
+// One decode: the layout and head grouping come in `a` (chunk and nsplit are set here).
+// Workgroups: one per (batch, key/value head, group of G query heads, split); partials and the
+// combine: one slot per (batch, query head).
+template <typename T, int D, int G, bool PAGED>
+FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* L, int B,
+                               dev::DecodeArgs a, int num_splits, hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     using Cfg = dev::DecCfg<T, D>;
-    const int nsplit = choose_splits(num_splits, BH, kv_len);
-    const int chunk = (kv_len + nsplit - 1) / nsplit;
-    const long long blocks = static_cast<long long>(BH) * nsplit;
+    const long long groups = static_cast<long long>(B) * a.Hkv * ((a.H / a.Hkv) / G);
+    const long long bhq = static_cast<long long>(B) * a.H;
+    if (groups > 0x7fffffffLL || bhq > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len);
+    a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
+    const long long blocks = groups * a.nsplit;
+    const long long slots = bhq * a.nsplit;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
 
-    const size_t acc_bytes = static_cast<size_t>(blocks) * D * sizeof(float);
-    const size_t ml_bytes = static_cast<size_t>(blocks) * sizeof(float2);
+    const size_t acc_bytes = static_cast<size_t>(slots) * D * sizeof(float);
+    const size_t ml_bytes = static_cast<size_t>(slots) * sizeof(float2);
     StreamWorkspace ws(stream);
     FlashAttentionError err = ws.alloc(acc_bytes + ml_bytes);
     if (err != FlashAttentionError::SUCCESS) return err;
@@ -275,48 +372,111 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws.get()) + acc_bytes);
 
     int tok = profile_kernel<T, D>("decode_split", stream);
-    hipLaunchKernelGGL((dev::decode_split_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const E*>(Q),
-                       reinterpret_cast<const E*>(K), reinterpret_cast<const E*>(V), part_acc,
-                       part_ml, kv_len, chunk, nsplit, scale * dev::kLog2e);
+    hipLaunchKernelGGL((dev::decode_split_kernel<T, D, G, PAGED>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0, stream,
+                       reinterpret_cast<const E*>(Q), reinterpret_cast<const E*>(K),
+                       reinterpret_cast<const E*>(V), part_acc, part_ml, a);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
     tok = profile_kernel<T, D>("decode_combine", stream);
-    hipLaunchKernelGGL((dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(BH)), dim3(D),
-                       0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L, nsplit);
+    hipLaunchKernelGGL((dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(bhq)),
+                       dim3(D), 0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L,
+                       a.nsplit);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
+}
+
+// G = the largest of 8, 4, 2, 1 that divides the query heads per key/value head: each K/V row
+// is then read once for G query heads.
+template <typename T, int D, bool PAGED>
+FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O, float* L, int B,
+                                       const dev::DecodeArgs& a, int num_splits,
+                                       hipStream_t stream) {
+    const int hpk = a.H / a.Hkv;
+    if (hpk % 8 == 0) return run_decode<T, D, 8, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+    if (hpk % 4 == 0) return run_decode<T, D, 4, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+    if (hpk % 2 == 0) return run_decode<T, D, 2, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+    return run_decode<T, D, 1, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+}
+
+template <typename T, bool PAGED>
+FlashAttentionError run_decode_dims(const T* Q, const T* K, const T* V, T* O, float* L, int B,
+                                    const dev::DecodeArgs& a, int head_dim, int num_splits,
+                                    hipStream_t stream) {
+    switch (head_dim) {
+        case 32:
+            return run_decode_grouped<T, 32, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+        case 64:
+            return run_decode_grouped<T, 64, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+        case 128:
+            return run_decode_grouped<T, 128, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+    }
+    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+}
+
+dev::DecodeArgs decode_args(int num_heads, int num_kv_heads, int kv_len, float scale) {
+    dev::DecodeArgs a{};
+    a.H = num_heads;
+    a.Hkv = num_kv_heads;
+    a.kv_len = kv_len;
+    a.page_size = 1;
+    a.max_pages = 0;
+    a.page_shift = -1;
+    a.c = scale * dev::kLog2e;
+    return a;
 }
 
 }  // namespace
 
 template <typename T>
+FlashAttentionError launch_decode_gqa(const T* Q, const T* K, const T* V, T* O, float* L,
+                                      int batch_size, int num_heads, int num_kv_heads,
+                                      int kv_len, int head_dim, float scale, int num_splits,
+                                      hipStream_t stream) {
+    const dev::DecodeArgs a = decode_args(num_heads, num_kv_heads, kv_len, scale);
+    return run_decode_dims<T, false>(Q, K, V, O, L, batch_size, a, head_dim, num_splits, stream);
+}
+
+template <typename T>
 FlashAttentionError launch_decode(const T* Q, const T* K, const T* V, T* O, float* L,
                                   int batch_size, int num_heads, int kv_len, int head_dim,
                                   float scale, int num_splits, hipStream_t stream) {
-    const long long bh = static_cast<long long>(batch_size) * num_heads;
-    if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    const int BH = static_cast<int>(bh);
-    switch (head_dim) {
-        case 32: return run_decode<T, 32>(Q, K, V, O, L, BH, kv_len, scale, num_splits, stream);
-        case 64: return run_decode<T, 64>(Q, K, V, O, L, BH, kv_len, scale, num_splits, stream);
-        case 128: return run_decode<T, 128>(Q, K, V, O, L, BH, kv_len, scale, num_splits, stream);
-    }
-    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+    return launch_decode_gqa<T>(Q, K, V, O, L, batch_size, num_heads, num_heads, kv_len,
+                                head_dim, scale, num_splits, stream);
 }
 
-template FlashAttentionError launch_decode<float>(const float*, const float*, const float*, float*,
-                                                  float*, int, int, int, int, float, int,
-                                                  hipStream_t);
-template FlashAttentionError launch_decode<__half>(const __half*, const __half*, const __half*,
-                                                   __half*, float*, int, int, int, int, float, int,
-                                                   hipStream_t);
-template FlashAttentionError launch_decode<__hip_bfloat16>(const __hip_bfloat16*,
-                                                           const __hip_bfloat16*,
-                                                           const __hip_bfloat16*, __hip_bfloat16*,
-                                                           float*, int, int, int, int, float, int,
-                                                           hipStream_t);
+template <typename T>
+FlashAttentionError launch_decode_paged(const T* Q, const T* K_cache, const T* V_cache, T* O,
+                                        float* L, const int* block_table, const int* seq_lens,
+                                        int batch_size, int num_heads, int num_kv_heads,
+                                        int page_size, int max_pages_per_seq, int head_dim,
+                                        float scale, int num_splits, hipStream_t stream) {
+    const long long cap = static_cast<long long>(page_size) * max_pages_per_seq;
+    if (cap > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    dev::DecodeArgs a = decode_args(num_heads, num_kv_heads, static_cast<int>(cap), scale);
+    a.block_table = block_table;
+    a.seq_lens = seq_lens;
+    a.page_size = page_size;
+    a.max_pages = max_pages_per_seq;
+    a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz(page_size) : -1;
+    return run_decode_dims<T, true>(Q, K_cache, V_cache, O, L, batch_size, a, head_dim,
+                                    num_splits, stream);
+}
+
+#define CUFLASH_DECODE_TYPE(T)                                                                  \
+    template FlashAttentionError launch_decode<T>(const T*, const T*, const T*, T*, float*, int, \
+                                                  int, int, int, float, int, hipStream_t);      \
+    template FlashAttentionError launch_decode_gqa<T>(const T*, const T*, const T*, T*, float*, \
+                                                      int, int, int, int, int, float, int,      \
+                                                      hipStream_t);                             \
+    template FlashAttentionError launch_decode_paged<T>(                                        \
+        const T*, const T*, const T*, T*, float*, const int*, const int*, int, int, int, int,   \
+        int, int, float, int, hipStream_t);
+CUFLASH_DECODE_TYPE(float)
+CUFLASH_DECODE_TYPE(__half)
+CUFLASH_DECODE_TYPE(__hip_bfloat16)
+#undef CUFLASH_DECODE_TYPE
 
 }  // namespace detail
 }  // namespace cuflash

@@ -30,6 +30,23 @@ FlashAttentionError launch_decode(const T* Q, const T* K, const T* V, T* O, floa
                                   int batch_size, int num_heads, int kv_len, int head_dim,
                                   float scale, int num_splits, hipStream_t stream);
 
+// Decode with num_kv_heads key/value heads shared by num_heads / num_kv_heads query heads each
+// (K, V [B, num_kv_heads, kv_len, D]).
+template <typename T>
+FlashAttentionError launch_decode_gqa(const T* Q, const T* K, const T* V, T* O, float* L,
+                                      int batch_size, int num_heads, int num_kv_heads,
+                                      int kv_len, int head_dim, float scale, int num_splits,
+                                      hipStream_t stream);
+
+// Decode over a paged cache K_cache, V_cache [num_pages, page_size, num_kv_heads, D] with
+// block_table [B, max_pages_per_seq] and seq_lens [B].
+template <typename T>
+FlashAttentionError launch_decode_paged(const T* Q, const T* K_cache, const T* V_cache, T* O,
+                                        float* L, const int* block_table, const int* seq_lens,
+                                        int batch_size, int num_heads, int num_kv_heads,
+                                        int page_size, int max_pages_per_seq, int head_dim,
+                                        float scale, int num_splits, hipStream_t stream);
+
 // Maps a HIP status after a launch or allocation to the library's error code.
 inline FlashAttentionError from_hip(hipError_t e) {
     if (e == hipSuccess) return FlashAttentionError::SUCCESS;

@@ -60,13 +60,20 @@ _BWD_ARGS = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 4 + [ctypes.c_float, ctypes
                                                           ctypes.c_void_p]
 _DEC_ARGS = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [ctypes.c_float, ctypes.c_int,
                                                           ctypes.c_void_p]
+_DEC_GQA_ARGS = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_int,
+                                                              ctypes.c_void_p]
+_DEC_PAGED_ARGS = [ctypes.c_void_p] * 7 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int,
+                                                                ctypes.c_void_p]
 
 EXPORTED_SYMBOLS = (
     "cuflash_attention_forward_f32", "cuflash_attention_forward_f16",
     "cuflash_attention_forward_bf16", "cuflash_attention_backward_f32",
     "cuflash_attention_backward_f16", "cuflash_attention_backward_bf16",
     "cuflash_attention_decode_f32", "cuflash_attention_decode_f16",
-    "cuflash_attention_decode_bf16", "cuflash_error_string", "cuflash_version",
+    "cuflash_attention_decode_bf16", "cuflash_attention_decode_gqa_f32",
+    "cuflash_attention_decode_gqa_f16", "cuflash_attention_decode_gqa_bf16",
+    "cuflash_attention_decode_paged_f32", "cuflash_attention_decode_paged_f16",
+    "cuflash_attention_decode_paged_bf16", "cuflash_error_string", "cuflash_version",
     "cuflash_profile_enable", "cuflash_profile_report",
 )
 
@@ -84,6 +91,10 @@ class CuFlashLibrary:
             bwd.argtypes, bwd.restype = _BWD_ARGS, ctypes.c_int
             dec = getattr(library, f"cuflash_attention_decode_{sfx}")
             dec.argtypes, dec.restype = _DEC_ARGS, ctypes.c_int
+            gqa = getattr(library, f"cuflash_attention_decode_gqa_{sfx}")
+            gqa.argtypes, gqa.restype = _DEC_GQA_ARGS, ctypes.c_int
+            paged = getattr(library, f"cuflash_attention_decode_paged_{sfx}")
+            paged.argtypes, paged.restype = _DEC_PAGED_ARGS, ctypes.c_int
         library.cuflash_error_string.argtypes = [ctypes.c_int]
         library.cuflash_error_string.restype = ctypes.c_char_p
         library.cuflash_version.argtypes = []
@@ -220,20 +231,62 @@ def flash_attention_backward(q, k, v, o, lse, do, scale: Optional[float] = None,
 def flash_attention_decode(q, k, v, scale: Optional[float] = None, num_splits: int = 0,
                            out=None, lse=None, stream=None,
                            lib: Optional[CuFlashLibrary] = None):
-    """Split-KV decode: q [B, H, 1, D], k/v [B, H, Lkv, D] -> O [B, H, 1, D], L [B, H, 1]."""
+    """Split-KV decode: q [B, H, 1, D], k/v [B, Hkv, Lkv, D] -> O [B, H, 1, D], L [B, H, 1].
+    Hkv == H calls cuflash_attention_decode_*, a divisor of H (grouped-query / multi-query
+    attention: query head h reads key/value head h // (H // Hkv)) cuflash_attention_decode_gqa_*."""
     torch = _torch()
     lib = lib or load_library()
     _check((q, k, v), q.dtype)
     B, H, one, D = q.shape
-    if one != 1 or k.shape[:2] != (B, H) or k.shape[3] != D or v.shape != k.shape:
-        raise ValueError("decode expects q [B,H,1,D] and k, v [B,H,Lkv,D]")
-    kv_len = k.shape[2]
+    if one != 1 or k.dim() != 4 or k.shape[0] != B or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError("decode expects q [B,H,1,D] and k, v [B,Hkv,Lkv,D]")
+    Hkv, kv_len = k.shape[1], k.shape[2]
     scale = float(D ** -0.5) if scale is None else float(scale)
     out = torch.empty_like(q) if out is None else out
     lse = torch.empty((B, H, 1), device=q.device, dtype=torch.float32) if lse is None else lse
-    status = lib.fn("decode", _suffix(q))(q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                          out.data_ptr(), lse.data_ptr(), B, H, kv_len, D, scale,
-                                          int(num_splits), _stream_ptr(stream))
+    if Hkv == H:
+        status = lib.fn("decode", _suffix(q))(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                              out.data_ptr(), lse.data_ptr(), B, H, kv_len, D,
+                                              scale, int(num_splits), _stream_ptr(stream))
+    else:
+        status = lib.fn("decode_gqa", _suffix(q))(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                  out.data_ptr(), lse.data_ptr(), B, H, Hkv,
+                                                  kv_len, D, scale, int(num_splits),
+                                                  _stream_ptr(stream))
+    _raise(lib, status)
+    return out, lse
+
+
+def flash_attention_decode_paged(q, k_cache, v_cache, block_table, seq_lens,
+                                 scale: Optional[float] = None, num_splits: int = 0, out=None,
+                                 lse=None, stream=None, lib: Optional[CuFlashLibrary] = None):
+    """Split-KV decode over a paged cache: q [B, H, 1, D]; k_cache, v_cache
+    [num_pages, page_size, Hkv, D]; block_table [B, max_pages] int32 (page of keys
+    [p * page_size, (p + 1) * page_size) of each sequence); seq_lens [B] int32.
+    -> O [B, H, 1, D], L [B, H, 1] (cuflash_attention_decode_paged_*)."""
+    torch = _torch()
+    lib = lib or load_library()
+    _check((q, k_cache, v_cache), q.dtype)
+    B, H, one, D = q.shape
+    if (one != 1 or k_cache.dim() != 4 or k_cache.shape[3] != D or v_cache.shape != k_cache.shape
+            or block_table.dim() != 2 or block_table.shape[0] != B
+            or tuple(seq_lens.shape) != (B,)):
+        raise ValueError("paged decode expects q [B,H,1,D], k/v cache [P,page,Hkv,D], "
+                         "block_table [B,max_pages], seq_lens [B]")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_table and seq_lens must be int32")
+    if not (block_table.is_contiguous() and seq_lens.is_contiguous()):
+        raise ValueError("block_table and seq_lens must be contiguous")
+    page_size, Hkv = k_cache.shape[1], k_cache.shape[2]
+    scale = float(D ** -0.5) if scale is None else float(scale)
+    out = torch.empty_like(q) if out is None else out
+    lse = torch.empty((B, H, 1), device=q.device, dtype=torch.float32) if lse is None else lse
+    status = lib.fn("decode_paged", _suffix(q))(q.data_ptr(), k_cache.data_ptr(),
+                                                v_cache.data_ptr(), out.data_ptr(),
+                                                lse.data_ptr(), block_table.data_ptr(),
+                                                seq_lens.data_ptr(), B, H, Hkv, page_size,
+                                                block_table.shape[1], D, scale, int(num_splits),
+                                                _stream_ptr(stream))
     _raise(lib, status)
     return out, lse
 
@@ -241,7 +294,7 @@ def flash_attention_decode(q, k, v, scale: Optional[float] = None, num_splits: i
 __all__ = [
     "CuFlashError", "CuFlashLibrary", "EXPORTED_SYMBOLS", "load_library",
     "candidate_library_paths", "flash_attention_forward", "flash_attention_backward",
-    "flash_attention_decode", "SUCCESS", "INVALID_DIMENSION", "DIMENSION_MISMATCH",
+    "flash_attention_decode", "flash_attention_decode_paged", "SUCCESS", "INVALID_DIMENSION", "DIMENSION_MISMATCH",
     "NULL_POINTER", "CUDA_ERROR", "OUT_OF_MEMORY", "UNSUPPORTED_HEAD_DIM", "UNSUPPORTED_DTYPE",
 ]
 

@@ -106,6 +106,46 @@ CUFLASH_EXPORT FlashAttentionError flash_attention_decode(
     float* L, int batch_size, int num_heads, int kv_len, int head_dim, float scale,
     int num_splits, hipStream_t stream = 0);
 
+// ---- Grouped-query and paged decode (additive; extensions of the decode above) ----
+// Grouped-query / multi-query attention: K, V have num_kv_heads heads, [batch_size,
+// num_kv_heads, kv_len, head_dim], and query head h attends with key/value head
+// h / (num_heads / num_kv_heads). num_heads must be a multiple of num_kv_heads
+// (DIMENSION_MISMATCH otherwise). num_kv_heads == num_heads is flash_attention_decode.
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_gqa(
+    const float* Q, const float* K, const float* V, float* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_gqa(
+    const __half* Q, const __half* K, const __half* V, __half* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_gqa(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V, __hip_bfloat16* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+
+// Paged KV cache: K_cache, V_cache [num_pages, page_size, num_kv_heads, head_dim];
+// block_table [batch_size, max_pages_per_seq] (int32) gives the page of keys
+// [p * page_size, (p + 1) * page_size) of each sequence; seq_lens [batch_size] (int32) its
+// length, clamped to [0, page_size * max_pages_per_seq]. Grouped-query heads as above. A
+// sequence of length 0 gives O = 0 and L = -inf. All of Q, K_cache, V_cache, O, L,
+// block_table and seq_lens are device pointers.
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_paged(
+    const float* Q, const float* K_cache, const float* V_cache, float* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_paged(
+    const __half* Q, const __half* K_cache, const __half* V_cache, __half* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_decode_paged(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K_cache, const __hip_bfloat16* V_cache, __hip_bfloat16* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream = 0);
+
 }  // namespace cuflash
 
 #ifdef __cplusplus
@@ -177,6 +217,32 @@ CUFLASH_EXPORT int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const 
                                                  float* L, int batch_size, int num_heads,
                                                  int kv_len, int head_dim, float scale,
                                                  int num_splits, hipStream_t stream);
+
+// Grouped-query and paged decode ABI (additive; same arguments as the C++ functions above).
+CUFLASH_EXPORT int cuflash_attention_decode_gqa_f32(
+    const float* Q, const float* K, const float* V, float* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_decode_paged_f32(
+    const float* Q, const float* K_cache, const float* V_cache, float* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_decode_gqa_f16(
+    const __half* Q, const __half* K, const __half* V, __half* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_decode_paged_f16(
+    const __half* Q, const __half* K_cache, const __half* V_cache, __half* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_decode_gqa_bf16(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V, __hip_bfloat16* O, float* L, int batch_size, int num_heads,
+    int num_kv_heads, int kv_len, int head_dim, float scale, int num_splits, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_decode_paged_bf16(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K_cache, const __hip_bfloat16* V_cache, __hip_bfloat16* O, float* L,
+    const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
+    int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
+    hipStream_t stream);
 
 // Library version string (CUFLASH_VERSION); additive.
 CUFLASH_EXPORT const char* cuflash_version(void);

@@ -35,7 +35,7 @@ def test_library_loads_from_reference_search_path(lib):
 
 def test_every_declared_symbol_is_exported(lib):
     declared = _declared_c_symbols()
-    assert len(declared) == 13, declared
+    assert len(declared) == 19, declared
     out = subprocess.run(["nm", "-D", "--defined-only", lib.path], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
@@ -144,6 +144,45 @@ def test_decode_validation(lib):
     assert dec(P, P, P, P, P, 1, 1, 16, 48, 1.0, 0, None) == cuflash_attn.UNSUPPORTED_HEAD_DIM
     assert dec(P, P, P, P, P, 1, 1, 16, 32, math.nan, 0, None) == cuflash_attn.INVALID_DIMENSION
     assert dec(P, P, P, P, P, 1, 1, 16, 32, 1.0, -1, None) == cuflash_attn.INVALID_DIMENSION
+
+
+def test_decode_gqa_validation(lib):
+    """Grouped-query decode: the decode checks, then num_kv_heads > 0 and a divisor of num_heads
+    (DIMENSION_MISMATCH otherwise). Every case returns before any GPU work."""
+    dec = lib.fn("decode_gqa", "bf16")
+    #            Q     K  V  O  L  B  H  Hkv kv  D   scale splits
+    assert dec(None, P, P, P, P, 1, 8, 2, 16, 64, 1.0, 0, None) == cuflash_attn.NULL_POINTER
+    assert dec(P, P, P, P, P, 1, 8, 2, 0, 64, 1.0, 0, None) == cuflash_attn.INVALID_DIMENSION
+    assert dec(P, P, P, P, P, 1, 8, 0, 16, 64, 1.0, 0, None) == cuflash_attn.INVALID_DIMENSION
+    assert dec(P, P, P, P, P, 1, 8, 3, 16, 64, 1.0, 0, None) == cuflash_attn.DIMENSION_MISMATCH
+    assert dec(P, P, P, P, P, 1, 8, 2, 16, 96, 1.0, 0, None) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+    assert dec(P, P, P, P, P, 1, 8, 2, 16, 64, -1.0, 0, None) == cuflash_attn.INVALID_DIMENSION
+    assert dec(P, P, P, P, P, 1, 8, 2, 16, 64, 1.0, -2, None) == cuflash_attn.INVALID_DIMENSION
+
+
+def test_decode_paged_validation(lib):
+    """Paged decode: every pointer including block_table and seq_lens non-null, page_size and
+    max_pages_per_seq positive and their product an int, then the grouped-query checks."""
+    dec = lib.fn("decode_paged", "f16")
+    #            Q  K  V  O  L  tab lens B  H  Hkv page maxp D  scale splits
+    ok = (P, P, P, P, P, P, P, 2, 8, 8, 16, 4, 128, 1.0, 0, None)
+    def call(**kw):
+        names = ["q", "k", "v", "o", "l", "tab", "lens", "b", "h", "hkv", "page", "maxp", "d",
+                 "scale", "splits", "stream"]
+        args = dict(zip(names, ok))
+        args.update(kw)
+        return dec(*[args[n] for n in names])
+    assert call(tab=None) == cuflash_attn.NULL_POINTER
+    assert call(lens=None) == cuflash_attn.NULL_POINTER
+    assert call(o=None) == cuflash_attn.NULL_POINTER
+    assert call(page=0) == cuflash_attn.INVALID_DIMENSION
+    assert call(maxp=-1) == cuflash_attn.INVALID_DIMENSION
+    assert call(page=1 << 16, maxp=1 << 16) == cuflash_attn.INVALID_DIMENSION
+    assert call(b=0) == cuflash_attn.INVALID_DIMENSION
+    assert call(hkv=3) == cuflash_attn.DIMENSION_MISMATCH
+    assert call(d=16) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+    assert call(scale=math.inf) == cuflash_attn.INVALID_DIMENSION
+    assert call(splits=-1) == cuflash_attn.INVALID_DIMENSION
 
 
 def test_candidate_paths_follow_reference_order(monkeypatch):
