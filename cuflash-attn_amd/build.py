@@ -4,7 +4,12 @@ The shared library lands in <repo>/build/libcuflash_attn.so, one of the paths th
 ctypes callers search (tests/integration/test_pytorch_comparison.py:158-180), with hidden default
 visibility so that only the CUFLASH_EXPORT symbols are exported (reference CMakeLists.txt:60-72).
 
-Usage: python cuflash-attn_amd/build.py [--jobs N]
+Usage: python cuflash-attn_amd/build.py [--jobs N] [--install PREFIX]
+
+--install PREFIX also installs the package the way the reference's CMake install does
+(CMakeLists.txt:268-315): headers under PREFIX/include, the library under PREFIX/lib, and a
+CMake package config under PREFIX/lib/cmake/cuflash_attn so that find_package(cuflash_attn
+CONFIG) provides the imported target cuflash::cuflash_attn.
 """
 
 from __future__ import annotations
@@ -90,12 +95,67 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     return LIB_PATH
 
 
+_CONFIG = """# cuflash_attn CMake package (installed by cuflash-attn_amd/build.py --install).
+# Imported target cuflash::cuflash_attn: the prebuilt libcuflash_attn.so for gfx950 and its
+# headers; consumers also get the HIP host runtime (hip::host) that the headers use.
+include(CMakeFindDependencyMacro)
+find_dependency(hip CONFIG PATHS /opt/rocm /opt/rocm/lib/cmake/hip)
+get_filename_component(_cuflash_prefix "${CMAKE_CURRENT_LIST_DIR}/../../.." ABSOLUTE)
+if(NOT TARGET cuflash::cuflash_attn)
+  add_library(cuflash::cuflash_attn SHARED IMPORTED)
+  set_target_properties(cuflash::cuflash_attn PROPERTIES
+    IMPORTED_LOCATION "${_cuflash_prefix}/lib/libcuflash_attn.so"
+    IMPORTED_SONAME "libcuflash_attn.so"
+    INTERFACE_INCLUDE_DIRECTORIES "${_cuflash_prefix}/include"
+    INTERFACE_LINK_LIBRARIES "hip::host")
+endif()
+unset(_cuflash_prefix)
+"""
+
+_CONFIG_VERSION = """set(PACKAGE_VERSION "@VERSION@")
+if(PACKAGE_FIND_VERSION VERSION_GREATER PACKAGE_VERSION)
+  set(PACKAGE_VERSION_COMPATIBLE FALSE)
+else()
+  set(PACKAGE_VERSION_COMPATIBLE TRUE)
+  if(PACKAGE_FIND_VERSION STREQUAL PACKAGE_VERSION)
+    set(PACKAGE_VERSION_EXACT TRUE)
+  endif()
+endif()
+"""
+
+
+def install(prefix: str, verbose: bool = True) -> str:
+    """Copies the built library and the public headers under `prefix` and writes the CMake
+    package config. Returns the config directory."""
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build first")
+    inc_dst = os.path.join(prefix, "include", "cuflash")
+    shutil.copytree(os.path.join(INCLUDE, "cuflash"), inc_dst, dirs_exist_ok=True)
+    lib_dir = os.path.join(prefix, "lib")
+    os.makedirs(lib_dir, exist_ok=True)
+    shutil.copy2(LIB_PATH, os.path.join(lib_dir, LIB_NAME))
+    cfg_dir = os.path.join(lib_dir, "cmake", "cuflash_attn")
+    os.makedirs(cfg_dir, exist_ok=True)
+    with open(os.path.join(INCLUDE, "cuflash", "version.h")) as f:
+        version = next(line.split('"')[1] for line in f if line.startswith("#define CUFLASH_VERSION "))
+    with open(os.path.join(cfg_dir, "cuflash_attnConfig.cmake"), "w") as f:
+        f.write(_CONFIG)
+    with open(os.path.join(cfg_dir, "cuflash_attnConfigVersion.cmake"), "w") as f:
+        f.write(_CONFIG_VERSION.replace("@VERSION@", version))
+    if verbose:
+        print(f"installed into {prefix}")
+    return cfg_dir
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--install", metavar="PREFIX", default=None)
     args = ap.parse_args()
     try:
         build(args.jobs)
+        if args.install:
+            install(args.install)
     except RuntimeError as e:
         print(e, file=sys.stderr)
         sys.exit(1)
