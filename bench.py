@@ -13,11 +13,15 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
 * roofline: the dominant kernel of the step, timed live with HIP events recorded around each of
   its launches on the launch stream (cuflash_profile_enable), against MI355X's dense bf16 MFMA
   peak. `rooflines` lists every kernel the same way.
+* ext: the extended forward / backward (cuflash_attention_{forward,backward}_ext_bf16) on a
+  prefill chunk against a KV cache with grouped-query heads, grouped-query training at the
+  config-3 size, and head_dim 96 and 256 at the config-3 size; reported beside the headline.
 * cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
   tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
   timed on a bounded sample of the config-3 workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-decode]
+                      [--no-ext]
 """
 
 from __future__ import annotations
@@ -104,6 +108,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-ext", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg3", "decode", "copy"), default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
     ap.add_argument("--cpu-seq", type=int, default=2048,
@@ -111,6 +116,79 @@ def parse():
     ap.add_argument("--cpu-heads", type=int, default=0,
                     help="heads in the CPU-baseline sample (default: one per host thread, <= 16)")
     return ap.parse_args()
+
+
+def causal_pairs(nq, nk):
+    """(query, key) pairs a bottom-right aligned causal mask keeps: query i sees i + nk - nq + 1
+    keys."""
+    return nq * (nk - nq) + nq * (nq + 1) / 2
+
+
+EXT_WORKLOADS = [
+    # name, B, H, Hkv, q_len, kv_len, D, backward too
+    ("prefill_chunk_gqa", 1, 32, 8, 2048, 16384, 128, False),
+    ("gqa_train", 2, 16, 4, 4096, 4096, 128, True),
+    ("head_dim_96", 2, 16, 16, 4096, 4096, 96, True),
+    ("head_dim_256", 2, 16, 16, 4096, 4096, 256, True),
+]
+
+
+def bench_ext(lib, torch, steps, stream):
+    """Times the extended entry points (bf16, causal) on EXT_WORKLOADS: per-launch forward and
+    backward time from the event hook, TFLOP/s with the reference's FLOP model over the (query,
+    key) pairs the mask keeps (forward 4 D per pair, backward 2.5 times that)."""
+    dev = torch.device("cuda:0")
+    fwd = lib.fn("forward_ext", "bf16")
+    bwd = lib.fn("backward_ext", "bf16")
+    sp = stream.cuda_stream
+    out = {}
+    for name, B, H, Hkv, nq, nk, D, with_bwd in EXT_WORKLOADS:
+        q = torch.randn((B, H, nq, D), device=dev).to(torch.bfloat16)
+        k = torch.randn((B, Hkv, nk, D), device=dev).to(torch.bfloat16)
+        v = torch.randn((B, Hkv, nk, D), device=dev).to(torch.bfloat16)
+        do = torch.randn((B, H, nq, D), device=dev).to(torch.bfloat16)
+        o, lse = torch.empty_like(q), torch.empty((B, H, nq), device=dev, dtype=torch.float32)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        scale = D ** -0.5
+
+        def run():
+            st = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H,
+                     Hkv, nq, nk, D, scale, True, sp)
+            if with_bwd:
+                st |= bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                          lse.data_ptr(), do.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                          dv.data_ptr(), B, H, Hkv, nq, nk, D, scale, True, sp)
+            if st != 0:
+                raise RuntimeError(f"{name}: library status {st}")
+
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
+        lib.profile_enable(True)
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        rep = lib.profile_report()
+        lib.profile_enable(False)
+        f_fwd = 4.0 * B * H * D * causal_pairs(nq, nk)
+        suffix = f"_bf16_d{D}"
+        k_ms = {lab[:-len(suffix)]: tot / n for lab, (n, tot) in rep.items()
+                if lab.endswith(suffix) and n}
+        rec = {"workload": f"bf16 causal B={B} H={H} Hkv={Hkv} q_len={nq} kv_len={nk} D={D}",
+               "fwd_ms": round(k_ms["forward"], 4),
+               "fwd_tflops": round(f_fwd / (k_ms["forward"] * 1e-3) / 1e12, 1)}
+        rec["fwd_frac"] = round(rec["fwd_tflops"] / PEAK_BF16_TFLOPS, 4)
+        if with_bwd:
+            b_ms = sum(v2 for k2, v2 in k_ms.items() if k2.startswith("backward"))
+            rec["bwd_ms"] = round(b_ms, 4)
+            rec["bwd_tflops"] = round(2.5 * f_fwd / (b_ms * 1e-3) / 1e12, 1)
+            rec["bwd_frac"] = round(rec["bwd_tflops"] / PEAK_BF16_TFLOPS, 4)
+            rec["step_tflops"] = round(3.5 * f_fwd / ((k_ms["forward"] + b_ms) * 1e-3) / 1e12, 1)
+        out[name] = rec
+        log(f"ext {name}: {rec}")
+        del q, k, v, do, o, lse, dq, dk, dv
+        torch.cuda.empty_cache()
+    return out
 
 
 def log(msg):
@@ -251,11 +329,18 @@ def main():
                   "pass": all(v2 <= 2e-2 for v2 in errs.values()),
                   "sample": f"heads {heads}, O/L all rows, grads every 61st row"}
 
+    del q, k, v, do, o, dq, dk, dv
+    torch.cuda.empty_cache()
+
+    # ---------------- extended entry points ----------------
+    ext = None
+    if not args.no_ext:
+        log("extended forward / backward workloads")
+        ext = bench_ext(lib, torch, max(3, args.steps // 4), stream)
+
     # ---------------- config 4: split-KV decode ----------------
     decode = None
     if not args.no_decode:
-        del q, k, v, do, o, dq, dk, dv
-        torch.cuda.empty_cache()
         Bd, Hd, LKV, Dd = CFG4["B"], CFG4["H"], CFG4["LKV"], CFG4["D"]
         log("generating config-4 inputs (torch generator on the GPU)")
         g = torch.Generator(device=dev)
@@ -412,6 +497,7 @@ def main():
         "rooflines": rooflines,
         "kernel_ms": {kk: round(vv, 4) for kk, vv in k_ms.items()},
         "decode": decode,
+        "ext": ext,
         "parity": parity,
         "cpu_baseline": cpu,
     }

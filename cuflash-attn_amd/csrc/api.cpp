@@ -109,6 +109,50 @@ FlashAttentionError check_decode_paged(const void* Q, const void* K, const void*
                             static_cast<int>(cap), head_dim, scale, num_splits);
 }
 
+// Extended forward / backward: the forward checks in the same order with num_kv_heads, q_len and
+// kv_len as dimensions and head_dim in {32, 64, 96, 128, 256}; then num_heads must be a
+// multiple of num_kv_heads, and a causal mask needs q_len <= kv_len (the queries are the last
+// q_len positions of the key sequence), else DIMENSION_MISMATCH.
+bool supported_head_dim_ext(int head_dim) {
+    return supported_head_dim(head_dim) || head_dim == 96 || head_dim == 256;
+}
+
+FlashAttentionError check_ext(const void* Q, const void* K, const void* V, const void* O,
+                              const void* L, int batch_size, int num_heads, int num_kv_heads,
+                              int q_len, int kv_len, int head_dim, float scale, bool causal) {
+    if (!Q || !K || !V || !O || !L) return FlashAttentionError::NULL_POINTER;
+    if (batch_size <= 0 || num_heads <= 0 || num_kv_heads <= 0 || q_len <= 0 || kv_len <= 0 ||
+        head_dim <= 0)
+        return FlashAttentionError::INVALID_DIMENSION;
+    if (!supported_head_dim_ext(head_dim)) return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+    if (!std::isfinite(scale) || scale < 0.0f) return FlashAttentionError::INVALID_DIMENSION;
+    if (num_heads % num_kv_heads != 0) return FlashAttentionError::DIMENSION_MISMATCH;
+    if (causal && q_len > kv_len) return FlashAttentionError::DIMENSION_MISMATCH;
+    return FlashAttentionError::SUCCESS;
+}
+
+template <typename T>
+FlashAttentionError forward_ext_impl(const T* Q, const T* K, const T* V, T* O, float* L, int b,
+                                     int h, int hkv, int nq, int nk, int d, float scale,
+                                     bool causal, hipStream_t stream) {
+    FlashAttentionError err = check_ext(Q, K, V, O, L, b, h, hkv, nq, nk, d, scale, causal);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    return detail::launch_forward_ext<T>(Q, K, V, O, L, b, h, hkv, nq, nk, d, scale, causal,
+                                         stream);
+}
+
+template <typename T>
+FlashAttentionError backward_ext_impl(const T* Q, const T* K, const T* V, const T* O,
+                                      const float* L, const T* dO, T* dQ, T* dK, T* dV, int b,
+                                      int h, int hkv, int nq, int nk, int d, float scale,
+                                      bool causal, hipStream_t stream) {
+    if (!dO || !dQ || !dK || !dV) return FlashAttentionError::NULL_POINTER;
+    FlashAttentionError err = check_ext(Q, K, V, O, L, b, h, hkv, nq, nk, d, scale, causal);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    return detail::launch_backward_ext<T>(Q, K, V, O, L, dO, dQ, dK, dV, b, h, hkv, nq, nk, d,
+                                          scale, causal, stream);
+}
+
 template <typename T>
 FlashAttentionError forward_impl(const T* Q, const T* K, const T* V, T* O, float* L, int b,
                                  int h, int n, int d, float scale, bool causal,
@@ -302,6 +346,28 @@ FlashAttentionError flash_attention_decode_paged(const __hip_bfloat16* Q, const 
                              scale, num_splits, stream);
 }
 
+// ===== Extended forward / backward (no reference counterpart) =====
+
+#define CUFLASH_EXT_OVERLOADS(T)                                                                 \
+    FlashAttentionError flash_attention_forward_ext(                                            \
+        const T* Q, const T* K, const T* V, T* O, float* L, int batch_size, int num_heads,       \
+        int num_kv_heads, int q_len, int kv_len, int head_dim, float scale, bool causal,         \
+        hipStream_t stream) {                                                                    \
+        return forward_ext_impl(Q, K, V, O, L, batch_size, num_heads, num_kv_heads, q_len,       \
+                                kv_len, head_dim, scale, causal, stream);                        \
+    }                                                                                            \
+    FlashAttentionError flash_attention_backward_ext(                                           \
+        const T* Q, const T* K, const T* V, const T* O, const float* L, const T* dO, T* dQ,      \
+        T* dK, T* dV, int batch_size, int num_heads, int num_kv_heads, int q_len, int kv_len,    \
+        int head_dim, float scale, bool causal, hipStream_t stream) {                            \
+        return backward_ext_impl(Q, K, V, O, L, dO, dQ, dK, dV, batch_size, num_heads,           \
+                                 num_kv_heads, q_len, kv_len, head_dim, scale, causal, stream);  \
+    }
+CUFLASH_EXT_OVERLOADS(float)
+CUFLASH_EXT_OVERLOADS(__half)
+CUFLASH_EXT_OVERLOADS(__hip_bfloat16)
+#undef CUFLASH_EXT_OVERLOADS
+
 }  // namespace cuflash
 
 // ===== C ABI (reference src/api/flash_attention_api.cu:186-242) =====
@@ -448,6 +514,28 @@ int cuflash_attention_decode_paged_bf16(const __hip_bfloat16* Q, const __hip_bfl
         Q, K_cache, V_cache, O, L, block_table, seq_lens, batch_size, num_heads, num_kv_heads,
         page_size, max_pages_per_seq, head_dim, scale, num_splits, stream));
 }
+
+#define CUFLASH_EXT_C_ABI(SFX, T)                                                                \
+    int cuflash_attention_forward_ext_##SFX(const T* Q, const T* K, const T* V, T* O, float* L,  \
+                                            int batch_size, int num_heads, int num_kv_heads,     \
+                                            int q_len, int kv_len, int head_dim, float scale,    \
+                                            bool causal, hipStream_t stream) {                   \
+        return static_cast<int>(cuflash::flash_attention_forward_ext(                            \
+            Q, K, V, O, L, batch_size, num_heads, num_kv_heads, q_len, kv_len, head_dim, scale,  \
+            causal, stream));                                                                    \
+    }                                                                                            \
+    int cuflash_attention_backward_ext_##SFX(                                                    \
+        const T* Q, const T* K, const T* V, const T* O, const float* L, const T* dO, T* dQ,      \
+        T* dK, T* dV, int batch_size, int num_heads, int num_kv_heads, int q_len, int kv_len,    \
+        int head_dim, float scale, bool causal, hipStream_t stream) {                            \
+        return static_cast<int>(cuflash::flash_attention_backward_ext(                           \
+            Q, K, V, O, L, dO, dQ, dK, dV, batch_size, num_heads, num_kv_heads, q_len, kv_len,   \
+            head_dim, scale, causal, stream));                                                   \
+    }
+CUFLASH_EXT_C_ABI(f32, float)
+CUFLASH_EXT_C_ABI(f16, __half)
+CUFLASH_EXT_C_ABI(bf16, __hip_bfloat16)
+#undef CUFLASH_EXT_C_ABI
 
 const char* cuflash_version(void) { return CUFLASH_VERSION; }
 

@@ -19,8 +19,13 @@
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
 // For fp16/bf16 at head_dim 128 the same steps run as delta_ld_kernel, then dq_d128 and
-// dkdv_d128 side by side in one launch (bwd_d128_kernel, section 4). Every path is deterministic: no atomics, and each output
-// element is written by exactly one lane.
+// dkdv_d128 side by side in one launch (bwd_d128_kernel, section 4). Every path is
+// deterministic: no atomics, and each output element is written by exactly one lane.
+//
+// Shapes: Q, O, dO, dQ are [BH, Nq, D], K, V, dK, dV are [BH / group, Nk, D] (query head bh
+// reads key/value head bh / group), L and D are [BH, Nq]. With a causal mask query i sees the
+// keys j <= i + coff, coff = Nk - Nq >= 0. The key-stationary kernels accumulate dK and dV of a
+// key/value head over all `group` query heads that read it, in registers, before one store.
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -98,6 +103,15 @@ __device__ __forceinline__ float dot16(u32x4 a, u32x4 b) {
     return s;
 }
 
+// Lanes per row of delta_kernel: the 16-byte chunks of a row, rounded up to a power of two so
+// that the xor-butterfly sum stays inside the row's lanes (head_dim 96: 12 chunks -> 16 lanes).
+template <int CHUNKS>
+constexpr int delta_lanes() {
+    int l = 1;
+    while (l < CHUNKS) l *= 2;
+    return l;
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     delta_kernel(const typename Mma<T>::elem* __restrict__ dO,
@@ -105,12 +119,14 @@ __global__ void __launch_bounds__(256)
                  long long rows) {
     using E = typename Mma<T>::elem;
     constexpr int VEC = 16 / static_cast<int>(sizeof(E));
-    constexpr int LPR = D / VEC;  // lanes per row
+    constexpr int CHUNKS = D / VEC;                 // 16-byte chunks per row
+    constexpr int LPR = delta_lanes<CHUNKS>();      // lanes per row
+    static_assert(LPR <= 64, "a row's lanes must fit in one wave");
     const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     const long long row = t / LPR;
     const int part = static_cast<int>(t % LPR);
     float s = 0.0f;
-    if (row < rows) {
+    if (row < rows && part < CHUNKS) {
         const size_t off = static_cast<size_t>(row) * D + part * VEC;
         s = dot16<T>(ld16(dO + off), ld16(O + off));
     }
@@ -134,7 +150,7 @@ struct DqCfg {
 // fp32 operands at D = 128 need more than the 256 registers a 2-wave budget allows.
 template <typename T, int D>
 constexpr int dq_min_waves() {
-    return (std::is_same<T, float>::value && D == 128) ? 1 : 2;
+    return ((std::is_same<T, float>::value && D >= 128) || D >= 256) ? 1 : 2;
 }
 
 template <typename T, int D>
@@ -143,8 +159,8 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
               const typename Mma<T>::elem* __restrict__ K,
               const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
               const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
-              typename Mma<T>::elem* __restrict__ dQ, int N, int nqb, float c, float scale,
-              int causal) {
+              typename Mma<T>::elem* __restrict__ dQ, int Nq, int Nk, int coff, int group,
+              int nqb, float c, float scale, int causal) {
     using M = Mma<T>;
     using E = typename M::elem;
     using frag = typename M::frag;
@@ -162,10 +178,11 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, dO, dQ
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
     const int q0 = qb * Cfg::BM + wave * 32;
     const int q = q0 + l32;
-    const bool q_ok = q < N;
+    const bool q_ok = q < Nq;
 
     frag qf[D / M::KW];
     frag of[D / M::KW];
@@ -178,22 +195,22 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
             of[ks] = M::row_operand(dO + head + static_cast<size_t>(q) * D + M::KW * ks);
         }
     }
-    // Rows past N get L = +inf so that P = exp(S - L) is exactly 0 there.
-    const float l2 = q_ok ? L[static_cast<size_t>(bh) * N + q] * kLog2e : INFINITY;
-    const float dq_row = q_ok ? Dl[static_cast<size_t>(bh) * N + q] : 0.0f;
+    // Rows past Nq get L = +inf so that P = exp(S - L) is exactly 0 there.
+    const float l2 = q_ok ? L[static_cast<size_t>(bh) * Nq + q] * kLog2e : INFINITY;
+    const float dq_row = q_ok ? Dl[static_cast<size_t>(bh) * Nq + q] : 0.0f;
 
     f32x16 acc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
 
-    const int kv_end = causal ? min(N, (qb + 1) * Cfg::BM) : N;
+    const int kv_end = causal ? min(Nk, (qb + 1) * Cfg::BM + coff) : Nk;
     const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
     TileCopy<E, Cfg::BN, D, Cfg::kThreads> kcp, vcp;
     const int col_off = M::col_lane_offset(Cfg::CP);
 
     if (nkb > 0) {
-        kcp.fetch(K + head, N, tid);
-        vcp.fetch(V + head, N, tid);
+        kcp.fetch(K + kv_head, Nk, tid);
+        vcp.fetch(V + kv_head, Nk, tid);
     }
     for (int kb = 0; kb < nkb; ++kb) {
         const int key0 = kb * Cfg::BN;
@@ -203,10 +220,11 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
         vcp.stage(Vs, Cfg::RP, tid);
         __syncthreads();
         if (kb + 1 < nkb) {
-            kcp.fetch(K + head + static_cast<size_t>(key0 + Cfg::BN) * D, N - key0 - Cfg::BN, tid);
-            vcp.fetch(V + head + static_cast<size_t>(key0 + Cfg::BN) * D, N - key0 - Cfg::BN, tid);
+            const size_t off = kv_head + static_cast<size_t>(key0 + Cfg::BN) * D;
+            kcp.fetch(K + off, Nk - key0 - Cfg::BN, tid);
+            vcp.fetch(V + off, Nk - key0 - Cfg::BN, tid);
         }
-        if (causal && key0 > q0 + 31) continue;
+        if (causal && key0 > q0 + 31 + coff) continue;
 
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
@@ -215,13 +233,13 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
             s = M::mma(M::row_operand(&Ks[l32 * Cfg::RP + M::KW * ks]), qf[ks], s);
             dp = M::mma(M::row_operand(&Vs[l32 * Cfg::RP + M::KW * ks]), of[ks], dp);
         }
-        const bool masked = (key0 + Cfg::BN > N) || (causal && key0 + Cfg::BN - 1 > q0);
+        const bool masked = (key0 + Cfg::BN > Nk) || (causal && key0 + Cfg::BN - 1 > q0 + coff);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             float p = fast_exp2(fmaf(s[r], c, -l2));
             if (masked) {
                 const int key = key0 + 8 * (r >> 2) + 4 * g2 + (r & 3);
-                if (key >= N || (causal && key > q)) p = 0.0f;
+                if (key >= Nk || (causal && key > q + coff)) p = 0.0f;
             }
             s[r] = p * (dp[r] - dq_row);
         }
@@ -276,7 +294,7 @@ __global__ void __launch_bounds__(256, 1)
                 const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
                 const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
                 typename Mma<T>::elem* __restrict__ dK, typename Mma<T>::elem* __restrict__ dV,
-                int N, int nkb, float c, float scale, int causal) {
+                int Nq, int Nk, int coff, int group, int nkb, float c, float scale, int causal) {
     using M = Mma<T>;
     using E = typename M::elem;
     using frag = typename M::frag;
@@ -289,20 +307,18 @@ __global__ void __launch_bounds__(256, 1)
     __shared__ __attribute__((aligned(16))) float Ds[Cfg::BM];
 
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = lid / nkb;
-    const int kb = lid % nkb;  // ascending: with a causal mask the first blocks carry the most work
+    const int bkv = lid / nkb;  // key/value head
+    const int kb = lid % nkb;   // ascending: with a causal mask the first blocks carry the most work
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
-    const float* Lh = L + static_cast<size_t>(bh) * N;
-    const float* Dh = Dl + static_cast<size_t>(bh) * N;
+    const size_t kv_head = static_cast<size_t>(bkv) * Nk * D;  // K, V, dK, dV
     const int k0 = kb * Cfg::BN + wave * 32;  // first key of this wave
     const int key = k0 + l32;                 // key row owned by this lane
-    const bool key_ok = key < N;
+    const bool key_ok = key < Nk;
 
     frag kf[D / M::KW];
     frag vf[D / M::KW];
@@ -311,8 +327,8 @@ __global__ void __launch_bounds__(256, 1)
         kf[ks] = M::zero();
         vf[ks] = M::zero();
         if (key_ok) {
-            kf[ks] = M::row_operand(K + head + static_cast<size_t>(key) * D + M::KW * ks);
-            vf[ks] = M::row_operand(V + head + static_cast<size_t>(key) * D + M::KW * ks);
+            kf[ks] = M::row_operand(K + kv_head + static_cast<size_t>(key) * D + M::KW * ks);
+            vf[ks] = M::row_operand(V + kv_head + static_cast<size_t>(key) * D + M::KW * ks);
         }
     }
 
@@ -324,27 +340,36 @@ __global__ void __launch_bounds__(256, 1)
         dv[dt] = f32x16{};
     }
 
-    const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
-    const int qb_begin = causal ? (kb * Cfg::BN) / Cfg::BM : 0;
+    // Query blocks [qb_begin, nqb) of each of the `group` query heads of this key/value head, as
+    // one sequence of n_it iterations (it -> head bkv * group + it / span, block
+    // qb_begin + it % span). With a causal mask the blocks before the first query that sees
+    // key kb * BN are skipped.
+    const int nqb = (Nq + Cfg::BM - 1) / Cfg::BM;
+    const int qb_begin = causal ? max(0, kb * Cfg::BN - coff) / Cfg::BM : 0;
+    const int span = nqb - qb_begin;
+    const int n_it = span > 0 ? group * span : 0;
     TileCopy<E, Cfg::BM, D, Cfg::kThreads> qcp, ocp;
     float lreg = 0.0f;
-    auto fetch = [&](int qb) {
-        const int r0 = qb * Cfg::BM;
-        qcp.fetch(Q + head + static_cast<size_t>(r0) * D, N - r0, tid);
-        ocp.fetch(dO + head + static_cast<size_t>(r0) * D, N - r0, tid);
+    auto fetch = [&](int it) {
+        const int bh = bkv * group + it / span;
+        const int r0 = (qb_begin + it % span) * Cfg::BM;
+        const size_t q_head = static_cast<size_t>(bh) * Nq * D;
+        qcp.fetch(Q + q_head + static_cast<size_t>(r0) * D, Nq - r0, tid);
+        ocp.fetch(dO + q_head + static_cast<size_t>(r0) * D, Nq - r0, tid);
         if (tid < 2 * Cfg::BM) {
             const int r = r0 + (tid % Cfg::BM);
+            const size_t row = static_cast<size_t>(bh) * Nq + r;
             if (tid < Cfg::BM)
-                lreg = r < N ? Lh[r] * kLog2e : INFINITY;  // rows past N: P = 0
+                lreg = r < Nq ? L[row] * kLog2e : INFINITY;  // rows past Nq: P = 0
             else
-                lreg = r < N ? Dh[r] : 0.0f;
+                lreg = r < Nq ? Dl[row] : 0.0f;
         }
     };
     const int col_off = M::col_lane_offset(Cfg::CP);
 
-    if (qb_begin < nqb) fetch(qb_begin);
-    for (int qb = qb_begin; qb < nqb; ++qb) {
-        const int q0 = qb * Cfg::BM;
+    if (n_it > 0) fetch(0);
+    for (int it = 0; it < n_it; ++it) {
+        const int q0 = (qb_begin + it % span) * Cfg::BM;
         __syncthreads();
         qcp.stage(Qs, Cfg::RP, tid);
         qcp.stage(Qc, Cfg::CP, tid);
@@ -355,7 +380,7 @@ __global__ void __launch_bounds__(256, 1)
         else if (tid < 2 * Cfg::BM)
             Ds[tid - Cfg::BM] = lreg;
         __syncthreads();
-        if (qb + 1 < nqb) fetch(qb + 1);
+        if (it + 1 < n_it) fetch(it + 1);
         // Waves whose keys all follow every query of the block still run (P = 0 there): a
         // branch around the MFMAs would make the compiler copy the dK/dV accumulators between
         // AGPRs and VGPRs on every iteration.
@@ -368,7 +393,7 @@ __global__ void __launch_bounds__(256, 1)
             s = M::mma(M::row_operand(&Qs[l32 * Cfg::RP + M::KW * ks]), kf[ks], s);
             dp = M::mma(M::row_operand(&Os[l32 * Cfg::RP + M::KW * ks]), vf[ks], dp);
         }
-        const bool masked = causal && (k0 + 31 > q0);
+        const bool masked = causal && (k0 + 31 > q0 + coff);
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             const f32x4 lv = *reinterpret_cast<const f32x4*>(&Ls[8 * a + 4 * g2]);
@@ -377,7 +402,7 @@ __global__ void __launch_bounds__(256, 1)
             for (int u = 0; u < 4; ++u) {
                 const int r = 4 * a + u;
                 float p = fast_exp2(fmaf(s[r], c, -lv[u]));
-                if (masked && key > q0 + 8 * a + 4 * g2 + u) p = 0.0f;
+                if (masked && key > q0 + 8 * a + 4 * g2 + u + coff) p = 0.0f;
                 s[r] = p;
                 dp[r] = p * (dp[r] - dv4[u]);
             }
@@ -396,8 +421,8 @@ __global__ void __launch_bounds__(256, 1)
     }
 
     if (key_ok) {
-        E* krow = dK + head + static_cast<size_t>(key) * D;
-        E* vrow = dV + head + static_cast<size_t>(key) * D;
+        E* krow = dK + kv_head + static_cast<size_t>(key) * D;
+        E* vrow = dV + kv_head + static_cast<size_t>(key) * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -431,7 +456,7 @@ __global__ void __launch_bounds__(256, 1)
 // ------------------------------------------------------------------------------------------
 // Row statistics for the D = 128 kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
-// without any masking.
+// without any masking. N is the query length.
 template <typename T>
 __global__ void __launch_bounds__(256)
     delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
@@ -479,7 +504,7 @@ __device__ __forceinline__ int grp_tr_sub() {  // transpose reads, without the r
     return (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 + (kq & 1) * 8;
 }
 
-// Key-stationary part of workgroup `bid` of BH * nkb (kb = 0, the most work, first); smem
+// Key-stationary part of workgroup `bid` of BHkv * nkb (kb = 0, the most work, first); smem
 // holds at least kDkdvLds bytes.
 constexpr int kDkdvLds = 2 * (2 * 8 * kGrp128 + 32 * 8);
 template <typename T>
@@ -489,8 +514,9 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                                           const float2* __restrict__ LD,
                                           const uint16_t* __restrict__ dO,
                                           uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
-                                          int N, int Npad, int nkb, int BH, float c, float scale,
-                                          int causal, int bid, unsigned char* smem) {
+                                          int Nq, int Nk, int coff, int group, int Npad,
+                                          int BHkv, float c, float scale, int causal, int bid,
+                                          unsigned char* smem) {
     constexpr int D = 128;
     constexpr int BN = 128;  // keys per workgroup (32 per wave)
     constexpr int BM = 32;   // query rows per block
@@ -500,21 +526,18 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
     static_assert(2 * SET == kDkdvLds, "LDS size");
     using frag = typename Elem<T>::frag;
 
-    int bh, kb;
-    head_rank_order(bid, BH, bh, kb);
+    int bkv, kb;  // key/value head, key block
+    head_rank_order(bid, BHkv, bkv, kb);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
-    const uint16_t* Qh = Q + head;
-    const uint16_t* Oh = dO + head;
-    const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
+    const size_t kv_head = static_cast<size_t>(bkv) * Nk * D;  // K, V, dK, dV
     const int kwg = kb * BN;
     const int k0 = kwg + wave * 32;
     const int key = k0 + l32;
-    const bool key_ok = key < N;
+    const bool key_ok = key < Nk;
 
     frag kf[D / 16];
     frag vf[D / 16];
@@ -522,22 +545,36 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
     for (int ks = 0; ks < D / 16; ++ks) {
         u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
         if (key_ok) {
-            kv = ld16(K + head + static_cast<size_t>(key) * D + 16 * ks + 8 * g2);
-            vv = ld16(V + head + static_cast<size_t>(key) * D + 16 * ks + 8 * g2);
+            kv = ld16(K + kv_head + static_cast<size_t>(key) * D + 16 * ks + 8 * g2);
+            vv = ld16(V + kv_head + static_cast<size_t>(key) * D + 16 * ks + 8 * g2);
         }
         kf[ks] = as_frag<T>(kv);
         vf[ks] = as_frag<T>(vv);
     }
 
+    // Query blocks [qb_begin, nqb) of each of the `group` query heads of this key/value head, as
+    // one sequence of n_it iterations (it -> head bkv * group + it / span, block
+    // qb_begin + it % span); with a causal mask the blocks before the first query that sees key
+    // kwg are skipped. qb_begin < nqb because that query is below Nq.
+    const int nqb = Npad / BM;
+    const int qb_begin = causal ? max(0, kwg - coff) / BM : 0;
+    const int span = nqb - qb_begin;
+    const int n_it = group * span;
+
     const int ld_row = lane & 3;
     const int ld_col = (lane >> 2) * 8;
-    auto load_block = [&](int qb, int b) {
-        const int r0 = qb * BM;
+    auto load_block = [&](int it, int b) {
+        const int bh = bkv * group + it / span;
+        const int r0 = (qb_begin + it % span) * BM;
+        const size_t q_head = static_cast<size_t>(bh) * Nq * D;
+        const uint16_t* Qh = Q + q_head;
+        const uint16_t* Oh = dO + q_head;
+        const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
         unsigned char* set = smem + b * SET;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int grp = wave + 4 * i;
-            const int row = min(r0 + 4 * grp + ld_row, N - 1);
+            const int row = min(r0 + 4 * grp + ld_row, Nq - 1);
             lds_dma16_async(Qh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
             lds_dma16_async(Oh + static_cast<size_t>(row) * D + ld_col, set + QT + grp * GRP);
         }
@@ -554,16 +591,14 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         dv[dt] = f32x16{};
     }
     const float cs = fmaxf(c, kFltMin);
-    const int nqb = Npad / BM;
-    const int qb_begin = causal ? kwg / BM : 0;
 
-    load_block(qb_begin, 0);
+    load_block(0, 0);
     int b = 0;
-    for (int qb = qb_begin; qb < nqb; ++qb, b ^= 1) {
-        const int q0 = qb * BM;
-        __builtin_amdgcn_s_waitcnt(0);  // block qb is in LDS
-        __syncthreads();                // ... for every wave; block qb - 1 is no longer read
-        if (qb + 1 < nqb) load_block(qb + 1, b ^ 1);
+    for (int it = 0; it < n_it; ++it, b ^= 1) {
+        const int q0 = (qb_begin + it % span) * BM;
+        __builtin_amdgcn_s_waitcnt(0);  // block it is in LDS
+        __syncthreads();                // ... for every wave; block it - 1 is no longer read
+        if (it + 1 < n_it) load_block(it + 1, b ^ 1);
         const unsigned char* qt = smem + b * SET;
         const unsigned char* ot = qt + QT;
         const float2* ldv = reinterpret_cast<const float2*>(qt + 2 * QT);
@@ -594,8 +629,8 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if ((causal && k0 + 31 > q0) || k0 + 31 >= N) {
-            const int lim = !key_ok ? 1 << 30 : (causal ? key - q0 - 4 * g2 : -1);
+        if ((causal && k0 + 31 > q0 + coff) || k0 + 31 >= Nk) {
+            const int lim = !key_ok ? 1 << 30 : (causal ? key - coff - q0 - 4 * g2 : -1);
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 s[r] = (8 * (r >> 2) + (r & 3) < lim) ? -INFINITY : s[r];
@@ -651,8 +686,8 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
     }
 
     if (key_ok) {
-        uint16_t* krow = dK + head + static_cast<size_t>(key) * D;
-        uint16_t* vrow = dV + head + static_cast<size_t>(key) * D;
+        uint16_t* krow = dK + kv_head + static_cast<size_t>(key) * D;
+        uint16_t* vrow = dV + kv_head + static_cast<size_t>(key) * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -679,9 +714,9 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
                                         const uint16_t* __restrict__ V,
                                         const float2* __restrict__ LD,
                                         const uint16_t* __restrict__ dO,
-                                        uint16_t* __restrict__ dQ, int N, int Npad, int nqb,
-                                        int BH, float c, float scale, int causal, int bid,
-                                        unsigned char* smem) {
+                                        uint16_t* __restrict__ dQ, int Nq, int Nk, int coff,
+                                        int group, int Npad, int nqb, int BH, float c,
+                                        float scale, int causal, int bid, unsigned char* smem) {
     constexpr int D = 128;
     constexpr int BM = 128;  // query rows per workgroup (32 per wave)
     constexpr int BN = 32;   // keys per block
@@ -699,12 +734,13 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
-    const uint16_t* Kh = K + head;
-    const uint16_t* Vh = V + head;
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, dO, dQ
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
     const int q0 = qb * BM + wave * 32;  // first query row of this wave
     const int q = q0 + l32;              // query row owned by this lane
-    const bool q_ok = q < N;
+    const bool q_ok = q < Nq;
 
     // Q^T and dO^T as B operands of S^T = K Q^T and dP^T = V dO^T (k = d).
     frag qf[D / 16];
@@ -730,7 +766,7 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int grp = wave + 4 * i;
-            const int row = min(r0 + 4 * grp + ld_row, N - 1);
+            const int row = min(r0 + 4 * grp + ld_row, Nk - 1);
             lds_dma16_async(Kh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
             lds_dma16_async(Vh + static_cast<size_t>(row) * D + ld_col, set + KT + grp * GRP);
         }
@@ -742,7 +778,7 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
     const float cs = fmaxf(c, kFltMin);
-    const int kv_end = causal ? min(N, (qb + 1) * BM) : N;
+    const int kv_end = causal ? min(Nk, (qb + 1) * BM + coff) : Nk;
     const int nkb = (kv_end + BN - 1) / BN;
 
     load_block(0, 0);
@@ -780,8 +816,8 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (key0 + BN > N || (causal && key0 + BN - 1 > q0)) {
-            const int lim = min(N, causal ? q + 1 : N) - key0 - 4 * g2;
+        if (key0 + BN > Nk || (causal && key0 + BN - 1 > q0 + coff)) {
+            const int lim = min(Nk, causal ? q + 1 + coff : Nk) - key0 - 4 * g2;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 s[r] = (8 * (r >> 2) + (r & 3) < lim) ? s[r] : -INFINITY;
@@ -836,24 +872,41 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
 // One launch for both passes (they are independent once delta_ld_kernel has run): workgroup
 // ids alternate between the dq and the dkdv grid, each in its own longest-first order, so the
 // two halves share the machine and their tails overlap instead of adding a kernel boundary.
+// The grid holds BH * nqb dq workgroups (128 query rows each) and BHkv * nkb dkdv workgroups
+// (128 keys each); when the counts differ, the ids past twice the smaller one run the rest of
+// the larger grid.
 template <typename T>
 __global__ void __launch_bounds__(256, 2)
     bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
-                    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int N, int Npad, int nb,
-                    int BH, float c, float scale, int causal) {
+                    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int Nq, int Nk,
+                    int coff, int group, int Npad, int nqb, int nkb, int BH, float c,
+                    float scale, int causal) {
     constexpr int kLds = kDkdvLds > kDqLds ? kDkdvLds : kDqLds;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
-    // nb query blocks of 128 rows = nb key blocks of 128 keys per head.
-    const int half = BH * nb;
+    const int BHkv = BH / group;
+    const int n_dq = BH * nqb;
+    const int n_dkdv = BHkv * nkb;
+    const int both = min(n_dq, n_dkdv);
     const int bid = blockIdx.x;
-    if (bid < 2 * half) {  // interleaved part
-        if (bid & 1)
-            dq_d128<T>(Q, K, V, LD, dO, dQ, N, Npad, nb, BH, c, scale, causal, bid >> 1, smem);
-        else
-            dkdv_d128<T>(Q, K, V, LD, dO, dK, dV, N, Npad, nb, BH, c, scale, causal, bid >> 1,
-                         smem);
+    bool is_dq;
+    int id;
+    if (bid < 2 * both) {  // interleaved part
+        is_dq = (bid & 1) != 0;
+        id = bid >> 1;
+    } else {
+        is_dq = n_dq > n_dkdv;
+        id = bid - both;
+    }
+    if (is_dq) {
+        if (id < n_dq)
+            dq_d128<T>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
+                       causal, id, smem);
+    } else {
+        if (id < n_dkdv)
+            dkdv_d128<T>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad, BHkv, c, scale,
+                         causal, id, smem);
     }
 }
 
@@ -863,11 +916,19 @@ namespace detail {
 
 namespace {
 
-// Generic path (fp32, and head_dim 32 / 64): delta, dq_kernel, dkdv_kernel.
+// Query/key extents of one launch (see the shape note at the top of this file).
+struct BwdShape {
+    int BH;     // query heads over the batch
+    int Nq;     // query rows per head
+    int Nk;     // key rows per key/value head
+    int group;  // query heads per key/value head
+};
+
+// Generic path (fp32, and head_dim 32 / 64 / 96 / 256): delta, dq_kernel, dkdv_kernel.
 template <typename T, int D>
 FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, const T* O,
                                           const float* L, const T* dO, T* dQ, T* dK, T* dV,
-                                          int BH, int N, float scale, bool causal,
+                                          const BwdShape& sh, float scale, bool causal,
                                           hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     const E* q = reinterpret_cast<const E*>(Q);
@@ -875,15 +936,16 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     const E* v = reinterpret_cast<const E*>(V);
     const E* o = reinterpret_cast<const E*>(O);
     const E* go = reinterpret_cast<const E*>(dO);
+    const int coff = sh.Nk - sh.Nq;
+    const int BHkv = sh.BH / sh.group;
 
-    const long long rows = static_cast<long long>(BH) * N;
+    const long long rows = static_cast<long long>(sh.BH) * sh.Nq;
     StreamWorkspace ws(stream);
     FlashAttentionError err = ws.alloc(static_cast<size_t>(rows) * sizeof(float));
     if (err != FlashAttentionError::SUCCESS) return err;
     float* delta = static_cast<float*>(ws.get());
 
-    constexpr int VEC = 16 / static_cast<int>(sizeof(E));
-    constexpr int LPR = D / VEC;
+    constexpr int LPR = dev::delta_lanes<D * static_cast<int>(sizeof(E)) / 16>();
     const long long dthreads = rows * LPR;
     const long long dblocks = (dthreads + 255) / 256;
     if (dblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
@@ -897,27 +959,28 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     const float c = scale * dev::kLog2e;
     {
         using Cfg = dev::DqCfg<T, D>;
-        const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
-        const long long blocks = static_cast<long long>(nqb) * BH;
+        const int nqb = (sh.Nq + Cfg::BM - 1) / Cfg::BM;
+        const long long blocks = static_cast<long long>(nqb) * sh.BH;
         if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
         tok = profile_kernel<T, D>("backward_dq", stream);
         hipLaunchKernelGGL((dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                            dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
-                           reinterpret_cast<E*>(dQ), N, nqb, c, scale, causal ? 1 : 0);
+                           reinterpret_cast<E*>(dQ), sh.Nq, sh.Nk, coff, sh.group, nqb, c, scale,
+                           causal ? 1 : 0);
         profile_end(tok, stream);
         err = from_hip(hipGetLastError());
         if (err != FlashAttentionError::SUCCESS) return err;
     }
     {
         using Cfg = dev::DkvCfg<T, D>;
-        const int nkb = (N + Cfg::BN - 1) / Cfg::BN;
-        const long long blocks = static_cast<long long>(nkb) * BH;
+        const int nkb = (sh.Nk + Cfg::BN - 1) / Cfg::BN;
+        const long long blocks = static_cast<long long>(nkb) * BHkv;
         if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
         tok = profile_kernel<T, D>("backward_dkdv", stream);
         hipLaunchKernelGGL((dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                            dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
-                           reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), N, nkb, c, scale,
-                           causal ? 1 : 0);
+                           reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk, coff,
+                           sh.group, nkb, c, scale, causal ? 1 : 0);
         profile_end(tok, stream);
         err = from_hip(hipGetLastError());
     }
@@ -928,21 +991,21 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
 template <typename T>
 FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* V, const T* O,
                                                const float* L, const T* dO, T* dQ, T* dK, T* dV,
-                                               int BH, int N, float scale, bool causal,
+                                               const BwdShape& sh, float scale, bool causal,
                                                hipStream_t stream) {
     constexpr int D = 128;
-    const int Npad = (N + 31) / 32 * 32;
-    const long long rows_pad = static_cast<long long>(BH) * Npad;
+    const int Npad = (sh.Nq + 31) / 32 * 32;
+    const long long rows_pad = static_cast<long long>(sh.BH) * Npad;
     StreamWorkspace ws(stream);
     FlashAttentionError err = ws.alloc(static_cast<size_t>(rows_pad) * sizeof(float2));
     if (err != FlashAttentionError::SUCCESS) return err;
     float2* ld = static_cast<float2*>(ws.get());
 
     const long long dblocks = (rows_pad * (D / 8) + 255) / 256;
-    const int nqb = (N + 127) / 128;
-    const int nkb = (N + 127) / 128;
-    const long long qblocks = static_cast<long long>(nqb) * BH;
-    const long long kblocks = static_cast<long long>(nkb) * BH;
+    const int nqb = (sh.Nq + 127) / 128;
+    const int nkb = (sh.Nk + 127) / 128;
+    const long long qblocks = static_cast<long long>(nqb) * sh.BH;
+    const long long kblocks = static_cast<long long>(nkb) * (sh.BH / sh.group);
     if (dblocks > 0x7fffffffLL || qblocks + kblocks > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
     const float c = scale * dev::kLog2e;
@@ -953,7 +1016,7 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
 
     int tok = profile_kernel<T, D>("backward_delta", stream);
     hipLaunchKernelGGL((dev::delta_ld_kernel<T>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
-                       0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, N, Npad,
+                       0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, sh.Nq, Npad,
                        rows_pad);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
@@ -962,21 +1025,54 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
     hipLaunchKernelGGL((dev::bwd_d128_kernel<T>), dim3(static_cast<unsigned>(qblocks + kblocks)),
                        dim3(256), 0, stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ),
-                       reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), N, Npad,
-                       nqb, BH, c, scale, causal ? 1 : 0);
+                       reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), sh.Nq,
+                       sh.Nk, sh.Nk - sh.Nq, sh.group, Npad, nqb, nkb, sh.BH, c, scale,
+                       causal ? 1 : 0);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 
 template <typename T, int D>
-FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O, const float* L,
-                                 const T* dO, T* dQ, T* dK, T* dV, int BH, int N, float scale,
-                                 bool causal, hipStream_t stream) {
+FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* O,
+                                   const float* L, const T* dO, T* dQ, T* dK, T* dV,
+                                   const BwdShape& sh, float scale, bool causal,
+                                   hipStream_t stream) {
     if constexpr (!std::is_same<T, float>::value && D == 128)
-        return run_backward_two_pass_d128<T>(Q, K, V, O, L, dO, dQ, dK, dV, BH, N, scale, causal,
+        return run_backward_two_pass_d128<T>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                              stream);
-    return run_backward_two_pass<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, BH, N, scale, causal,
-                                       stream);
+    else
+        return run_backward_two_pass<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                           stream);
+}
+
+// head_dim dispatch; `extended` admits the head dims beyond the reference's 32 / 64 / 128.
+template <typename T>
+FlashAttentionError run_backward(const T* Q, const T* K, const T* V, const T* O, const float* L,
+                                 const T* dO, T* dQ, T* dK, T* dV, const BwdShape& sh,
+                                 int head_dim, bool extended, float scale, bool causal,
+                                 hipStream_t stream) {
+    switch (head_dim) {
+        case 32:
+            return run_backward_d<T, 32>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                         stream);
+        case 64:
+            return run_backward_d<T, 64>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                         stream);
+        case 128:
+            return run_backward_d<T, 128>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                          stream);
+        case 96:
+            if (extended)
+                return run_backward_d<T, 96>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                             stream);
+            break;
+        case 256:
+            if (extended)
+                return run_backward_d<T, 256>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                              stream);
+            break;
+    }
+    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
 }
 
 }  // namespace
@@ -988,33 +1084,35 @@ FlashAttentionError launch_backward(const T* Q, const T* K, const T* V, const T*
                                     float scale, bool causal, hipStream_t stream) {
     const long long bh = static_cast<long long>(batch_size) * num_heads;
     if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    const int BH = static_cast<int>(bh);
-    switch (head_dim) {
-        case 32:
-            return run_backward<T, 32>(Q, K, V, O, L, dO, dQ, dK, dV, BH, seq_len, scale, causal,
-                                       stream);
-        case 64:
-            return run_backward<T, 64>(Q, K, V, O, L, dO, dQ, dK, dV, BH, seq_len, scale, causal,
-                                       stream);
-        case 128:
-            return run_backward<T, 128>(Q, K, V, O, L, dO, dQ, dK, dV, BH, seq_len, scale, causal,
-                                        stream);
-    }
-    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+    const BwdShape sh{static_cast<int>(bh), seq_len, seq_len, 1};
+    return run_backward<T>(Q, K, V, O, L, dO, dQ, dK, dV, sh, head_dim, false, scale, causal,
+                           stream);
 }
 
-template FlashAttentionError launch_backward<float>(const float*, const float*, const float*,
-                                                    const float*, const float*, const float*,
-                                                    float*, float*, float*, int, int, int, int,
-                                                    float, bool, hipStream_t);
-template FlashAttentionError launch_backward<__half>(const __half*, const __half*, const __half*,
-                                                     const __half*, const float*, const __half*,
-                                                     __half*, __half*, __half*, int, int, int, int,
-                                                     float, bool, hipStream_t);
-template FlashAttentionError launch_backward<__hip_bfloat16>(
-    const __hip_bfloat16*, const __hip_bfloat16*, const __hip_bfloat16*, const __hip_bfloat16*,
-    const float*, const __hip_bfloat16*, __hip_bfloat16*, __hip_bfloat16*, __hip_bfloat16*, int,
-    int, int, int, float, bool, hipStream_t);
+template <typename T>
+FlashAttentionError launch_backward_ext(const T* Q, const T* K, const T* V, const T* O,
+                                        const float* L, const T* dO, T* dQ, T* dK, T* dV,
+                                        int batch_size, int num_heads, int num_kv_heads,
+                                        int q_len, int kv_len, int head_dim, float scale,
+                                        bool causal, hipStream_t stream) {
+    const long long bh = static_cast<long long>(batch_size) * num_heads;
+    if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const BwdShape sh{static_cast<int>(bh), q_len, kv_len, num_heads / num_kv_heads};
+    return run_backward<T>(Q, K, V, O, L, dO, dQ, dK, dV, sh, head_dim, true, scale, causal,
+                           stream);
+}
+
+#define CUFLASH_BACKWARD_TYPE(T)                                                              \
+    template FlashAttentionError launch_backward<T>(const T*, const T*, const T*, const T*,   \
+                                                    const float*, const T*, T*, T*, T*, int,  \
+                                                    int, int, int, float, bool, hipStream_t); \
+    template FlashAttentionError launch_backward_ext<T>(                                      \
+        const T*, const T*, const T*, const T*, const float*, const T*, T*, T*, T*, int, int,  \
+        int, int, int, int, float, bool, hipStream_t);
+CUFLASH_BACKWARD_TYPE(float)
+CUFLASH_BACKWARD_TYPE(__half)
+CUFLASH_BACKWARD_TYPE(__hip_bfloat16)
+#undef CUFLASH_BACKWARD_TYPE
 
 }  // namespace detail
 }  // namespace cuflash

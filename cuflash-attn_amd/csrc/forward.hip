@@ -17,6 +17,11 @@
 // registers). Each lane therefore owns one query row of O, and the softmax rescale is a per-lane
 // multiply. The next K/V block is fetched into registers while the current one is consumed.
 // Causal launches process the longest query blocks first; blocks of one head share an XCD.
+//
+// Shapes: Q and O are [BH, Nq, D], K and V are [BH / group, Nk, D] (query head bh reads
+// key/value head bh / group), L is [BH, Nq]. With a causal mask query i sees the keys
+// j <= i + coff, coff = Nk - Nq >= 0 (the queries are the last Nq positions of the key
+// sequence; Nq == Nk gives the usual j <= i).
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -45,11 +50,18 @@ struct Fwd16Cfg {
     static_assert(BN * kChunksPerRow % kThreads == 0, "tile copy must divide evenly");
 };
 
+// Two workgroups per CU, except at head_dim 256 (O, Q^T and the scores need more than the
+// 256 registers per lane that two workgroups of four waves leave).
+template <int D>
+constexpr int fwd_min_waves() {
+    return D >= 256 ? 1 : 2;
+}
+
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
     fwd16_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ L,
-                 int N, int nqb, float c, int causal) {
+                 int Nq, int Nk, int coff, int group, int nqb, float c, int causal) {
     using Cfg = Fwd16Cfg<D>;
     using frag = typename Elem<T>::frag;
     __shared__ __attribute__((aligned(16))) uint16_t Ks[Cfg::BN * Cfg::KP];
@@ -64,10 +76,11 @@ __global__ void __launch_bounds__(256, 2)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
     const uint16_t* Qh = Q + head;
-    const uint16_t* Kh = K + head;
-    const uint16_t* Vh = V + head;
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
 
     const int q0 = qb * Cfg::BM + wave * 32;  // first query row of this wave
     const int q = q0 + l32;                   // query row owned by this lane
@@ -77,7 +90,7 @@ __global__ void __launch_bounds__(256, 2)
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (q < N) v = ld16(Qh + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        if (q < Nq) v = ld16(Qh + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
         qf[ks] = as_frag<T>(v);
     }
 
@@ -87,7 +100,7 @@ __global__ void __launch_bounds__(256, 2)
     float m = -INFINITY;
     float l = 0.0f;
 
-    const int kv_end = causal ? min(N, (qb + 1) * Cfg::BM) : N;
+    const int kv_end = causal ? min(Nk, (qb + 1) * Cfg::BM + coff) : Nk;
     const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
 
     u32x4 kreg[Cfg::kChunksPerThread];
@@ -99,7 +112,7 @@ __global__ void __launch_bounds__(256, 2)
             const int row = id / Cfg::kChunksPerRow;
             const int col = (id % Cfg::kChunksPerRow) * 8;
             const int key = kb * Cfg::BN + row;
-            if (key < N) {
+            if (key < Nk) {
                 const size_t off = static_cast<size_t>(key) * D + col;
                 kreg[i] = ld16(Kh + off);
                 vreg[i] = ld16(Vh + off);
@@ -145,11 +158,11 @@ __global__ void __launch_bounds__(256, 2)
             }
         }
 
-        const bool masked = (key0 + Cfg::BN > N) || (causal && key0 + Cfg::BN - 1 > q0);
+        const bool masked = (key0 + Cfg::BN > Nk) || (causal && key0 + Cfg::BN - 1 > q0 + coff);
         float alpha;
         const bool rescale =
-            masked ? softmax_step<2, true>(s, key0, q, N, causal != 0, c, m, l, alpha)
-                   : softmax_step<2, false>(s, key0, q, N, causal != 0, c, m, l, alpha);
+            masked ? softmax_step<2, true>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha)
+                   : softmax_step<2, false>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha);
         if (rescale) {
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
@@ -173,7 +186,7 @@ __global__ void __launch_bounds__(256, 2)
 
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
     l += xor_shuffle(l, 32);
-    if (q < N) {
+    if (q < Nq) {
         const float inv = 1.0f / l;
         uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
 #pragma unroll
@@ -186,7 +199,7 @@ __global__ void __launch_bounds__(256, 2)
                 st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
             }
         }
-        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
     }
 }
 
@@ -215,7 +228,8 @@ template <typename T, int NW>
 __global__ void __launch_bounds__(64 * NW, 8 / NW)
     fwd16_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
-                      float* __restrict__ L, int N, int nqb, float c, int causal) {
+                      float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
+                      float c, int causal) {
     constexpr int D = 128;
     constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
     constexpr int BN = 64;
@@ -237,9 +251,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
-    const uint16_t* Kh = K + head;
-    const uint16_t* Vh = V + head;
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
     const int q0 = qb * BM + wave * 32;  // first query row of this wave
     const int q = q0 + l32;              // query row owned by this lane
 
@@ -247,30 +262,30 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (q < N) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        if (q < Nq) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
         qf[ks] = as_frag<T>(v);
     }
 
-    const int kv_end = causal ? min(N, (qb + 1) * BM) : N;
+    const int kv_end = causal ? min(Nk, (qb + 1) * BM + coff) : Nk;
     const int nkb = (kv_end + BN - 1) / BN;
 
     // Loads of one 64-row tile: wave w fills groups w, w + NW, ... (kParts of them). Rows past
-    // N are clamped to row N - 1 (finite values; their scores are masked). The loads are issued from
+    // Nk are clamped to row Nk - 1 (finite values; their scores are masked). The loads are issued from
     // inline assembly, so the compiler adds no waits for them and keeps partial LDS waits for
     // the operand reads; the loop orders every LDS access itself (s_waitcnt(0) and a barrier
     // before a tile is read and before a buffer is refilled).
-    // A tile that lies inside [0, N) is addressed as a scalar base plus a fixed per-lane offset.
+    // A tile that lies inside [0, Nk) is addressed as a scalar base plus a fixed per-lane offset.
     const int ld_row = lane & 3;
     const int ld_col = (lane >> 2) * 8;
     const unsigned ld_voff = static_cast<unsigned>(((4 * wave + ld_row) * D + ld_col) * 2);
     // Part i (0..kParts-1) of a tile load: this wave's group wave + NW i.
     auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
-        if (key0 + BN <= N) {
+        if (key0 + BN <= Nk) {
             lds_dma16_async_s(src + static_cast<size_t>(key0 + 4 * NW * i) * D, ld_voff,
                               dst + (wave + NW * i) * GRP);
         } else {
             const int grp = wave + NW * i;
-            const int row = min(key0 + 4 * grp + ld_row, N - 1);
+            const int row = min(key0 + 4 * grp + ld_row, Nk - 1);
             lds_dma16_async(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
         }
     };
@@ -304,9 +319,9 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // for scale = 0 (where FLT_MIN leaves every p at 1 and L at log(count), as with 0).
     const float cs = fmaxf(c, kFltMin);
 
-    // Keys past N and, with a causal mask, keys after this lane's row get s = -inf.
+    // Keys past Nk and, with a causal mask, keys after this lane's row get s = -inf.
     auto mask_scores = [&](f32x16 (&s)[2], int key0) {
-        const int lim = min(N, causal ? q + 1 : N) - key0 - 4 * g2;
+        const int lim = min(Nk, causal ? q + 1 + coff : Nk) - key0 - 4 * g2;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -342,9 +357,11 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
         return tr_frag_at<T>(a0, a0 + 2 * GRP);
     };
 
-    // Blocks that need masking: keys past N, and with a causal mask the blocks that reach past
-    // this wave's first row.
-    auto needs_mask = [&](int key0) { return key0 + BN > N || (causal && key0 + BN - 1 > q0); };
+    // Blocks that need masking: keys past Nk, and with a causal mask the blocks that reach past
+    // the last key this wave's first row sees.
+    auto needs_mask = [&](int key0) {
+        return key0 + BN > Nk || (causal && key0 + BN - 1 > q0 + coff);
+    };
 
     // Exponential of score r of tile t, and the rounding of tile t's group h of eight scores
     // to T (the P operand of key group 2 t + h).
@@ -482,7 +499,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
     l = pair_sum(l);
-    if (q < N) {
+    if (q < Nq) {
         const float inv = 1.0f / l;
         uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
 #pragma unroll
@@ -495,7 +512,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                 st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
             }
         }
-        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
     }
 }
 
@@ -515,10 +532,10 @@ struct Fwd32Cfg {
 };
 
 template <int D>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
     fwd32_kernel(const float* __restrict__ Q, const float* __restrict__ K,
-                 const float* __restrict__ V, float* __restrict__ O, float* __restrict__ L, int N,
-                 int nqb, float c, int causal) {
+                 const float* __restrict__ V, float* __restrict__ O, float* __restrict__ L,
+                 int Nq, int Nk, int coff, int group, int nqb, float c, int causal) {
     using Cfg = Fwd32Cfg<D>;
     __shared__ __attribute__((aligned(16))) float Ks[Cfg::BN * Cfg::KP];
     __shared__ __attribute__((aligned(16))) float Vs[Cfg::BN * Cfg::VP];
@@ -532,10 +549,11 @@ __global__ void __launch_bounds__(256, 2)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
-    const size_t head = static_cast<size_t>(bh) * N * D;
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
     const float* Qh = Q + head;
-    const float* Kh = K + head;
-    const float* Vh = V + head;
+    const float* Kh = K + kv_head;
+    const float* Vh = V + kv_head;
     const int q0 = qb * Cfg::BM + wave * 32;
     const int q = q0 + l32;
 
@@ -544,7 +562,7 @@ __global__ void __launch_bounds__(256, 2)
 #pragma unroll
     for (int i = 0; i < D / 8; ++i) {
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (q < N) v = __builtin_bit_cast(f32x4, ld16(Qh + static_cast<size_t>(q) * D + (D / 2) * g2 + 4 * i));
+        if (q < Nq) v = __builtin_bit_cast(f32x4, ld16(Qh + static_cast<size_t>(q) * D + (D / 2) * g2 + 4 * i));
 #pragma unroll
         for (int u = 0; u < 4; ++u) qf[4 * i + u] = v[u];
     }
@@ -555,7 +573,7 @@ __global__ void __launch_bounds__(256, 2)
     float m = -INFINITY;
     float l = 0.0f;
 
-    const int kv_end = causal ? min(N, (qb + 1) * Cfg::BM) : N;
+    const int kv_end = causal ? min(Nk, (qb + 1) * Cfg::BM + coff) : Nk;
     const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
 
     u32x4 kreg[Cfg::kChunksPerThread];
@@ -567,7 +585,7 @@ __global__ void __launch_bounds__(256, 2)
             const int row = id / Cfg::kChunksPerRow;
             const int col = (id % Cfg::kChunksPerRow) * 4;
             const int key = kb * Cfg::BN + row;
-            if (key < N) {
+            if (key < Nk) {
                 const size_t off = static_cast<size_t>(key) * D + col;
                 kreg[i] = ld16(Kh + off);
                 vreg[i] = ld16(Vh + off);
@@ -607,11 +625,11 @@ __global__ void __launch_bounds__(256, 2)
             for (int u = 0; u < 4; ++u) s[0] = mma_f32(a4[u], qf[4 * i + u], s[0]);
         }
 
-        const bool masked = (key0 + Cfg::BN > N) || (causal && key0 + Cfg::BN - 1 > q0);
+        const bool masked = (key0 + Cfg::BN > Nk) || (causal && key0 + Cfg::BN - 1 > q0 + coff);
         float alpha;
         const bool rescale =
-            masked ? softmax_step<1, true>(s, key0, q, N, causal != 0, c, m, l, alpha)
-                   : softmax_step<1, false>(s, key0, q, N, causal != 0, c, m, l, alpha);
+            masked ? softmax_step<1, true>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha)
+                   : softmax_step<1, false>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha);
         if (rescale) {
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
@@ -630,7 +648,7 @@ __global__ void __launch_bounds__(256, 2)
     }
 
     l += xor_shuffle(l, 32);
-    if (q < N) {
+    if (q < Nq) {
         const float inv = 1.0f / l;
         float* Orow = O + head + static_cast<size_t>(q) * D;
 #pragma unroll
@@ -645,7 +663,7 @@ __global__ void __launch_bounds__(256, 2)
                 st16(Orow + 32 * dt + 8 * a + 4 * g2, __builtin_bit_cast(u32x4, w));
             }
         }
-        if (g2 == 0) L[static_cast<size_t>(bh) * N + q] = (m + fast_log2(l)) * kLn2;
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
     }
 }
 
@@ -655,28 +673,41 @@ namespace detail {
 
 namespace {
 
+// Query/key extents of one launch (see the shape note at the top of this file).
+struct FwdShape {
+    int BH;     // query heads over the batch
+    int Nq;     // query rows per head
+    int Nk;     // key rows per key/value head
+    int group;  // query heads per key/value head
+};
+
 template <typename T, int D>
-FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, float* L, int BH,
-                                  int N, float scale, bool causal, hipStream_t stream) {
+FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, float* L,
+                                  const FwdShape& sh, float scale, bool causal,
+                                  hipStream_t stream) {
     using Cfg = dev::Fwd16Cfg<D>;
     constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
     constexpr int BM = D == 128 ? 32 * kWaves128 : Cfg::BM;
-    const int nqb = (N + BM - 1) / BM;
-    const long long blocks = static_cast<long long>(nqb) * BH;
+    const int nqb = (sh.Nq + BM - 1) / BM;
+    const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const int coff = sh.Nk - sh.Nq;
     const int tok = profile_kernel<T, D>("forward", stream);
     if constexpr (D == 128) {
         hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0, stream,
+                           reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
-                           L, N, nqb, scale * dev::kLog2e, causal ? 1 : 0);
+                           L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
+                           causal ? 1 : 0);
     } else {
         hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
                            dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
-                           L, N, nqb, scale * dev::kLog2e, causal ? 1 : 0);
+                           L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
+                           causal ? 1 : 0);
     }
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
@@ -684,18 +715,47 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
 
 template <int D>
 FlashAttentionError run_forward32(const float* Q, const float* K, const float* V, float* O,
-                                  float* L, int BH, int N, float scale, bool causal,
+                                  float* L, const FwdShape& sh, float scale, bool causal,
                                   hipStream_t stream) {
     using Cfg = dev::Fwd32Cfg<D>;
-    const int nqb = (N + Cfg::BM - 1) / Cfg::BM;
-    const long long blocks = static_cast<long long>(nqb) * BH;
+    const int nqb = (sh.Nq + Cfg::BM - 1) / Cfg::BM;
+    const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int tok = profile_kernel<float, D>("forward", stream);
     hipLaunchKernelGGL((dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, N, nqb,
-                       scale * dev::kLog2e, causal ? 1 : 0);
+                       dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, sh.Nq, sh.Nk,
+                       sh.Nk - sh.Nq, sh.group, nqb, scale * dev::kLog2e, causal ? 1 : 0);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
+}
+
+template <typename T, int D>
+FlashAttentionError run_forward_d(const T* Q, const T* K, const T* V, T* O, float* L,
+                                  const FwdShape& sh, float scale, bool causal,
+                                  hipStream_t stream) {
+    if constexpr (std::is_same<T, float>::value)
+        return run_forward32<D>(Q, K, V, O, L, sh, scale, causal, stream);
+    else
+        return run_forward16<T, D>(Q, K, V, O, L, sh, scale, causal, stream);
+}
+
+// head_dim dispatch; `extended` admits the head dims beyond the reference's 32 / 64 / 128.
+template <typename T>
+FlashAttentionError run_forward(const T* Q, const T* K, const T* V, T* O, float* L,
+                                const FwdShape& sh, int head_dim, bool extended, float scale,
+                                bool causal, hipStream_t stream) {
+    switch (head_dim) {
+        case 32: return run_forward_d<T, 32>(Q, K, V, O, L, sh, scale, causal, stream);
+        case 64: return run_forward_d<T, 64>(Q, K, V, O, L, sh, scale, causal, stream);
+        case 128: return run_forward_d<T, 128>(Q, K, V, O, L, sh, scale, causal, stream);
+        case 96:
+            if (extended) return run_forward_d<T, 96>(Q, K, V, O, L, sh, scale, causal, stream);
+            break;
+        case 256:
+            if (extended) return run_forward_d<T, 256>(Q, K, V, O, L, sh, scale, causal, stream);
+            break;
+    }
+    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
 }
 
 }  // namespace
@@ -706,35 +766,32 @@ FlashAttentionError launch_forward(const T* Q, const T* K, const T* V, T* O, flo
                                    float scale, bool causal, hipStream_t stream) {
     const long long bh = static_cast<long long>(batch_size) * num_heads;
     if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    const int BH = static_cast<int>(bh);
-    if constexpr (std::is_same<T, float>::value) {
-        switch (head_dim) {
-            case 32: return run_forward32<32>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-            case 64: return run_forward32<64>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-            case 128: return run_forward32<128>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-        }
-    } else {
-        switch (head_dim) {
-            case 32: return run_forward16<T, 32>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-            case 64: return run_forward16<T, 64>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-            case 128:
-                return run_forward16<T, 128>(Q, K, V, O, L, BH, seq_len, scale, causal, stream);
-        }
-    }
-    return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
+    const FwdShape sh{static_cast<int>(bh), seq_len, seq_len, 1};
+    return run_forward<T>(Q, K, V, O, L, sh, head_dim, false, scale, causal, stream);
 }
 
-template FlashAttentionError launch_forward<float>(const float*, const float*, const float*,
-                                                   float*, float*, int, int, int, int, float, bool,
-                                                   hipStream_t);
-template FlashAttentionError launch_forward<__half>(const __half*, const __half*, const __half*,
-                                                    __half*, float*, int, int, int, int, float,
-                                                    bool, hipStream_t);
-template FlashAttentionError launch_forward<__hip_bfloat16>(const __hip_bfloat16*,
-                                                            const __hip_bfloat16*,
-                                                            const __hip_bfloat16*,
-                                                            __hip_bfloat16*, float*, int, int, int,
-                                                            int, float, bool, hipStream_t);
+template <typename T>
+FlashAttentionError launch_forward_ext(const T* Q, const T* K, const T* V, T* O, float* L,
+                                       int batch_size, int num_heads, int num_kv_heads,
+                                       int q_len, int kv_len, int head_dim, float scale,
+                                       bool causal, hipStream_t stream) {
+    const long long bh = static_cast<long long>(batch_size) * num_heads;
+    if (bh > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    const FwdShape sh{static_cast<int>(bh), q_len, kv_len, num_heads / num_kv_heads};
+    return run_forward<T>(Q, K, V, O, L, sh, head_dim, true, scale, causal, stream);
+}
+
+#define CUFLASH_FORWARD_TYPE(T)                                                                 \
+    template FlashAttentionError launch_forward<T>(const T*, const T*, const T*, T*, float*,    \
+                                                   int, int, int, int, float, bool,             \
+                                                   hipStream_t);                                \
+    template FlashAttentionError launch_forward_ext<T>(const T*, const T*, const T*, T*,        \
+                                                       float*, int, int, int, int, int, int,    \
+                                                       float, bool, hipStream_t);
+CUFLASH_FORWARD_TYPE(float)
+CUFLASH_FORWARD_TYPE(__half)
+CUFLASH_FORWARD_TYPE(__hip_bfloat16)
+#undef CUFLASH_FORWARD_TYPE
 
 }  // namespace detail
 }  // namespace cuflash

@@ -24,6 +24,23 @@ FlashAttentionError launch_backward(const T* Q, const T* K, const T* V, const T*
                                     int batch_size, int num_heads, int seq_len, int head_dim,
                                     float scale, bool causal, hipStream_t stream);
 
+// Forward and backward with separate query / key lengths, num_kv_heads key/value heads shared by
+// num_heads / num_kv_heads query heads each, and head_dim in {32, 64, 96, 128, 256}
+// (no reference counterpart). Q, O, dO, dQ are [B, num_heads, q_len, D], K, V, dK, dV are
+// [B, num_kv_heads, kv_len, D]; a causal mask is aligned to the end of the key sequence
+// (query i sees keys j <= i + kv_len - q_len) and needs q_len <= kv_len.
+template <typename T>
+FlashAttentionError launch_forward_ext(const T* Q, const T* K, const T* V, T* O, float* L,
+                                       int batch_size, int num_heads, int num_kv_heads,
+                                       int q_len, int kv_len, int head_dim, float scale,
+                                       bool causal, hipStream_t stream);
+template <typename T>
+FlashAttentionError launch_backward_ext(const T* Q, const T* K, const T* V, const T* O,
+                                        const float* L, const T* dO, T* dQ, T* dK, T* dV,
+                                        int batch_size, int num_heads, int num_kv_heads,
+                                        int q_len, int kv_len, int head_dim, float scale,
+                                        bool causal, hipStream_t stream);
+
 // Split-KV decode (no reference counterpart).
 template <typename T>
 FlashAttentionError launch_decode(const T* Q, const T* K, const T* V, T* O, float* L,

@@ -64,6 +64,10 @@ _DEC_GQA_ARGS = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 5 + [ctypes.c_float, ct
                                                               ctypes.c_void_p]
 _DEC_PAGED_ARGS = [ctypes.c_void_p] * 7 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int,
                                                                 ctypes.c_void_p]
+_FWD_EXT_ARGS = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_bool,
+                                                              ctypes.c_void_p]
+_BWD_EXT_ARGS = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_bool,
+                                                              ctypes.c_void_p]
 
 EXPORTED_SYMBOLS = (
     "cuflash_attention_forward_f32", "cuflash_attention_forward_f16",
@@ -73,7 +77,10 @@ EXPORTED_SYMBOLS = (
     "cuflash_attention_decode_bf16", "cuflash_attention_decode_gqa_f32",
     "cuflash_attention_decode_gqa_f16", "cuflash_attention_decode_gqa_bf16",
     "cuflash_attention_decode_paged_f32", "cuflash_attention_decode_paged_f16",
-    "cuflash_attention_decode_paged_bf16", "cuflash_error_string", "cuflash_version",
+    "cuflash_attention_decode_paged_bf16", "cuflash_attention_forward_ext_f32",
+    "cuflash_attention_forward_ext_f16", "cuflash_attention_forward_ext_bf16",
+    "cuflash_attention_backward_ext_f32", "cuflash_attention_backward_ext_f16",
+    "cuflash_attention_backward_ext_bf16", "cuflash_error_string", "cuflash_version",
     "cuflash_profile_enable", "cuflash_profile_report",
 )
 
@@ -95,6 +102,10 @@ class CuFlashLibrary:
             gqa.argtypes, gqa.restype = _DEC_GQA_ARGS, ctypes.c_int
             paged = getattr(library, f"cuflash_attention_decode_paged_{sfx}")
             paged.argtypes, paged.restype = _DEC_PAGED_ARGS, ctypes.c_int
+            fwd_ext = getattr(library, f"cuflash_attention_forward_ext_{sfx}")
+            fwd_ext.argtypes, fwd_ext.restype = _FWD_EXT_ARGS, ctypes.c_int
+            bwd_ext = getattr(library, f"cuflash_attention_backward_ext_{sfx}")
+            bwd_ext.argtypes, bwd_ext.restype = _BWD_EXT_ARGS, ctypes.c_int
         library.cuflash_error_string.argtypes = [ctypes.c_int]
         library.cuflash_error_string.restype = ctypes.c_char_p
         library.cuflash_version.argtypes = []
@@ -228,6 +239,56 @@ def flash_attention_backward(q, k, v, o, lse, do, scale: Optional[float] = None,
     return dq, dk, dv
 
 
+def _ext_shapes(q, k, v):
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError("expected q [B,H,Nq,D] and k, v [B,Hkv,Nk,D]")
+    B, H, Nq, D = q.shape
+    if k.shape[0] != B or k.shape[3] != D:
+        raise ValueError("q and k, v differ in batch or head_dim")
+    return B, H, k.shape[1], Nq, k.shape[2], D
+
+
+def flash_attention_forward_ext(q, k, v, scale: Optional[float] = None, causal: bool = False,
+                                out=None, lse=None, stream=None,
+                                lib: Optional[CuFlashLibrary] = None):
+    """Forward with q [B, H, Nq, D] and k, v [B, Hkv, Nk, D] (Hkv a divisor of H; query head h
+    reads key/value head h // (H // Hkv)), D in {32, 64, 96, 128, 256}; a causal mask lets
+    query i see keys j <= i + Nk - Nq (cuflash_attention_forward_ext_*).
+    -> O [B, H, Nq, D], L float32 [B, H, Nq]."""
+    torch = _torch()
+    lib = lib or load_library()
+    _check((q, k, v), q.dtype)
+    B, H, Hkv, Nq, Nk, D = _ext_shapes(q, k, v)
+    scale = float(D ** -0.5) if scale is None else float(scale)
+    out = torch.empty_like(q) if out is None else out
+    lse = torch.empty((B, H, Nq), device=q.device, dtype=torch.float32) if lse is None else lse
+    status = lib.fn("forward_ext", _suffix(q))(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                               out.data_ptr(), lse.data_ptr(), B, H, Hkv, Nq,
+                                               Nk, D, scale, bool(causal), _stream_ptr(stream))
+    _raise(lib, status)
+    return out, lse
+
+
+def flash_attention_backward_ext(q, k, v, o, lse, do, scale: Optional[float] = None,
+                                 causal: bool = False, stream=None,
+                                 lib: Optional[CuFlashLibrary] = None):
+    """dQ [B, H, Nq, D], dK, dV [B, Hkv, Nk, D] for the shapes of flash_attention_forward_ext
+    (dK, dV of a key/value head summed over its query heads; cuflash_attention_backward_ext_*)."""
+    torch = _torch()
+    lib = lib or load_library()
+    _check((q, k, v, o, do), q.dtype)
+    B, H, Hkv, Nq, Nk, D = _ext_shapes(q, k, v)
+    scale = float(D ** -0.5) if scale is None else float(scale)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    status = lib.fn("backward_ext", _suffix(q))(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+                                                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H,
+                                                Hkv, Nq, Nk, D, scale, bool(causal),
+                                                _stream_ptr(stream))
+    _raise(lib, status)
+    return dq, dk, dv
+
+
 def flash_attention_decode(q, k, v, scale: Optional[float] = None, num_splits: int = 0,
                            out=None, lse=None, stream=None,
                            lib: Optional[CuFlashLibrary] = None):
@@ -294,7 +355,8 @@ def flash_attention_decode_paged(q, k_cache, v_cache, block_table, seq_lens,
 __all__ = [
     "CuFlashError", "CuFlashLibrary", "EXPORTED_SYMBOLS", "load_library",
     "candidate_library_paths", "flash_attention_forward", "flash_attention_backward",
-    "flash_attention_decode", "flash_attention_decode_paged", "SUCCESS", "INVALID_DIMENSION", "DIMENSION_MISMATCH",
+    "flash_attention_forward_ext", "flash_attention_backward_ext", "flash_attention_decode",
+    "flash_attention_decode_paged", "SUCCESS", "INVALID_DIMENSION", "DIMENSION_MISMATCH",
     "NULL_POINTER", "CUDA_ERROR", "OUT_OF_MEMORY", "UNSUPPORTED_HEAD_DIM", "UNSUPPORTED_DTYPE",
 ]
 

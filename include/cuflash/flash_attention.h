@@ -146,6 +146,49 @@ CUFLASH_EXPORT FlashAttentionError flash_attention_decode_paged(
     int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
     hipStream_t stream = 0);
 
+// ---- Extended forward / backward (additive; no reference counterpart) ----
+// The forward and backward above with
+//  * separate query and key/value lengths: Q, O, dO, dQ are [batch_size, num_heads, q_len,
+//    head_dim], K, V, dK, dV are [batch_size, num_kv_heads, kv_len, head_dim], L is
+//    [batch_size, num_heads, q_len] (prefill against a KV cache, cross-attention);
+//  * grouped-query / multi-query heads: query head h reads key/value head
+//    h / (num_heads / num_kv_heads); dK and dV of a key/value head are the sums over its query
+//    heads. num_heads must be a multiple of num_kv_heads (DIMENSION_MISMATCH otherwise);
+//  * head_dim in {32, 64, 96, 128, 256} (the functions above keep the reference's 32 / 64 / 128
+//    and report UNSUPPORTED_HEAD_DIM for the others; so do these, with the same message).
+// A causal mask is aligned to the end of the key sequence: query i sees keys
+// j <= i + kv_len - q_len, so it needs q_len <= kv_len (DIMENSION_MISMATCH otherwise);
+// q_len == kv_len is the usual mask. With num_kv_heads == num_heads, q_len == kv_len and a
+// head_dim of 32 / 64 / 128 the results equal flash_attention_forward / _backward.
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward_ext(
+    const float* Q, const float* K, const float* V, float* O, float* L, int batch_size,
+    int num_heads, int num_kv_heads, int q_len, int kv_len, int head_dim, float scale,
+    bool causal = false, hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward_ext(
+    const __half* Q, const __half* K, const __half* V, __half* O, float* L, int batch_size,
+    int num_heads, int num_kv_heads, int q_len, int kv_len, int head_dim, float scale,
+    bool causal = false, hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_forward_ext(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    __hip_bfloat16* O, float* L, int batch_size, int num_heads, int num_kv_heads, int q_len,
+    int kv_len, int head_dim, float scale, bool causal = false, hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward_ext(
+    const float* Q, const float* K, const float* V, const float* O, const float* L,
+    const float* dO, float* dQ, float* dK, float* dV, int batch_size, int num_heads,
+    int num_kv_heads, int q_len, int kv_len, int head_dim, float scale, bool causal = false,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward_ext(
+    const __half* Q, const __half* K, const __half* V, const __half* O, const float* L,
+    const __half* dO, __half* dQ, __half* dK, __half* dV, int batch_size, int num_heads,
+    int num_kv_heads, int q_len, int kv_len, int head_dim, float scale, bool causal = false,
+    hipStream_t stream = 0);
+CUFLASH_EXPORT FlashAttentionError flash_attention_backward_ext(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    const __hip_bfloat16* O, const float* L, const __hip_bfloat16* dO, __hip_bfloat16* dQ,
+    __hip_bfloat16* dK, __hip_bfloat16* dV, int batch_size, int num_heads, int num_kv_heads,
+    int q_len, int kv_len, int head_dim, float scale, bool causal = false,
+    hipStream_t stream = 0);
+
 }  // namespace cuflash
 
 #ifdef __cplusplus
@@ -243,6 +286,35 @@ CUFLASH_EXPORT int cuflash_attention_decode_paged_bf16(
     const int* block_table, const int* seq_lens, int batch_size, int num_heads, int num_kv_heads,
     int page_size, int max_pages_per_seq, int head_dim, float scale, int num_splits,
     hipStream_t stream);
+
+// Extended forward / backward ABI (additive; same arguments as the C++ functions above).
+CUFLASH_EXPORT int cuflash_attention_forward_ext_f32(
+    const float* Q, const float* K, const float* V, float* O, float* L, int batch_size,
+    int num_heads, int num_kv_heads, int q_len, int kv_len, int head_dim, float scale,
+    bool causal, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_backward_ext_f32(
+    const float* Q, const float* K, const float* V, const float* O, const float* L,
+    const float* dO, float* dQ, float* dK, float* dV, int batch_size, int num_heads,
+    int num_kv_heads, int q_len, int kv_len, int head_dim, float scale, bool causal,
+    hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_forward_ext_f16(
+    const __half* Q, const __half* K, const __half* V, __half* O, float* L, int batch_size,
+    int num_heads, int num_kv_heads, int q_len, int kv_len, int head_dim, float scale,
+    bool causal, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_backward_ext_f16(
+    const __half* Q, const __half* K, const __half* V, const __half* O, const float* L,
+    const __half* dO, __half* dQ, __half* dK, __half* dV, int batch_size, int num_heads,
+    int num_kv_heads, int q_len, int kv_len, int head_dim, float scale, bool causal,
+    hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_forward_ext_bf16(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    __hip_bfloat16* O, float* L, int batch_size, int num_heads, int num_kv_heads, int q_len,
+    int kv_len, int head_dim, float scale, bool causal, hipStream_t stream);
+CUFLASH_EXPORT int cuflash_attention_backward_ext_bf16(
+    const __hip_bfloat16* Q, const __hip_bfloat16* K, const __hip_bfloat16* V,
+    const __hip_bfloat16* O, const float* L, const __hip_bfloat16* dO, __hip_bfloat16* dQ,
+    __hip_bfloat16* dK, __hip_bfloat16* dV, int batch_size, int num_heads, int num_kv_heads,
+    int q_len, int kv_len, int head_dim, float scale, bool causal, hipStream_t stream);
 
 // Library version string (CUFLASH_VERSION); additive.
 CUFLASH_EXPORT const char* cuflash_version(void);

@@ -46,7 +46,7 @@ def _load():
     lib = ctypes.CDLL(_LIB_PATH)
     lib.oracle_forward.argtypes = [_fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64,
                                    ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int]
-    lib.oracle_backward.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64,
+    lib.oracle_backward.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64,
                                     ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.oracle_backward_rows.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64,
                                          ctypes.c_double, ctypes.c_int, _ip, _i64, _ip, _i64,
@@ -103,12 +103,17 @@ def forward(q, k, v, scale: float, causal: bool, nthreads: int | None = None, mu
 
 def backward(q, k, v, do, scale: float, causal: bool, nthreads: int | None = None,
              mutation: int = 0):
-    """dQ, dK, dV in fp64 arithmetic, P materialized (reference test_backward.cu:21-127)."""
+    """dQ, dK, dV in fp64 arithmetic, P materialized (reference test_backward.cu:21-127).
+
+    K and V may have a different key count Nk; causal masks keys j > i + Nk - Nq (Nq <= Nk).
+    """
     q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
-    B, H, N, D = q.shape
-    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    assert k.shape == (B, H, Nk, D) and v.shape == k.shape and do.shape == q.shape
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(k)
     rc = _load().oracle_backward(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(dq), _ptr(dk),
-                                 _ptr(dv), B * H, N, D, float(scale), int(bool(causal)),
+                                 _ptr(dv), B * H, Nq, Nk, D, float(scale), int(bool(causal)),
                                  nthreads or default_threads(), mutation)
     assert rc == 0
     return dq, dk, dv

@@ -14,6 +14,8 @@
  *                          (tests/unit/test_backward.cu:21-127): P, dV = P^T dO, dP = dO V^T,
  *                          D_i = sum_j P_ij dP_ij, dS = P (dP - D) (0 where masked),
  *                          dQ = scale dS K, dK = scale dS^T Q. Materializes P per head.
+ *                          Q and K may differ in length (Nq <= Nk when causal), as in the
+ *                          forward.
  *   oracle_backward_rows   Row-streaming form of the same gradients for selected query rows
  *                          (dQ) and key rows (dK, dV), O(N*D) memory: first a pass computing
  *                          L_i and O_i, then D_i = dO_i . O_i (the identity the reference kernel
@@ -35,6 +37,7 @@
  *   4 = scale dropped from dK
  *   5 = max not subtracted before exp (drops the LSE shift; L = log sum exp(s))
  *   6 = dV from P instead of P^T (dV_j = sum_i P_ji dO_i)
+ *   7 = causal mask aligned to the start of the key sequence (j > i) when Nq != Nk
  */
 
 #include <math.h>
@@ -85,7 +88,8 @@ static void parallel_for(i64 n, int nthreads, range_fn fn, void* ctx) {
 
 static int masked_key(i64 i, i64 j, i64 Nq, i64 Nk, int causal, int mutation) {
     if (!causal) return 0;
-    const i64 lim = i + (Nk - Nq); /* bottom-right aligned; j > i when Nq == Nk */
+    /* bottom-right aligned (j > i when Nq == Nk); mutation 7 aligns it top-left instead */
+    const i64 lim = (mutation == 7) ? i : i + (Nk - Nq);
     return mutation == 2 ? (j >= lim) : (j > lim);
 }
 
@@ -152,6 +156,7 @@ static void fwd_rows(void* p, i64 begin, i64 end) {
 int oracle_forward(const float* Q, const float* K, const float* V, float* O, float* L, i64 BH,
                    i64 Nq, i64 Nk, i64 D, double scale, int causal, int nthreads, int mutation) {
     if (!Q || !K || !V || !O || BH <= 0 || Nq <= 0 || Nk <= 0 || D <= 0) return 1;
+    if (causal && Nq > Nk) return 1; /* rows without any visible key */
     fwd_ctx c = {Q, K, V, O, L, Nq, Nk, D, scale, causal, mutation};
     parallel_for(BH * Nq, nthreads, fwd_rows, &c);
     return 0;
@@ -159,86 +164,88 @@ int oracle_forward(const float* Q, const float* K, const float* V, float* O, flo
 
 /* ------------------------------------------------------------------------------------------ */
 /* backward, materialized (direct restatement of test_backward.cu:21-127)                      */
+/* Q, dO, dQ are [BH, Nq, D]; K, V, dK, dV are [BH, Nk, D]; causal masks j > i + Nk - Nq.      */
 /* ------------------------------------------------------------------------------------------ */
 typedef struct {
     const float *Q, *K, *V, *dO;
     float *dQ, *dK, *dV;
-    i64 N, D;
+    i64 Nq, Nk, D;
     double scale;
     int causal, mutation;
 } bwd_ctx;
 
 static void bwd_heads(void* p, i64 begin, i64 end) {
     bwd_ctx* c = (bwd_ctx*)p;
-    const i64 N = c->N, D = c->D;
-    double* P = (double*)malloc(sizeof(double) * (size_t)(N * N));
-    double* dP = (double*)malloc(sizeof(double) * (size_t)(N * N));
+    const i64 Nq = c->Nq, Nk = c->Nk, D = c->D;
+    double* P = (double*)malloc(sizeof(double) * (size_t)(Nq * Nk));
+    double* dP = (double*)malloc(sizeof(double) * (size_t)(Nq * Nk));
     for (i64 bh = begin; bh < end; ++bh) {
-        const i64 off = bh * N * D;
-        const float *Qh = c->Q + off, *Kh = c->K + off, *Vh = c->V + off, *dOh = c->dO + off;
+        const i64 qoff = bh * Nq * D, koff = bh * Nk * D;
+        const float *Qh = c->Q + qoff, *Kh = c->K + koff, *Vh = c->V + koff, *dOh = c->dO + qoff;
         /* P */
-        for (i64 i = 0; i < N; ++i) {
+        for (i64 i = 0; i < Nq; ++i) {
             double m = -INFINITY;
-            double* Pi = P + i * N;
-            for (i64 j = 0; j < N; ++j) {
-                if (masked_key(i, j, N, N, c->causal, c->mutation)) {
+            double* Pi = P + i * Nk;
+            for (i64 j = 0; j < Nk; ++j) {
+                if (masked_key(i, j, Nq, Nk, c->causal, c->mutation)) {
                     Pi[j] = -INFINITY;
                 } else {
-                    Pi[j] = score(Qh + i * D, Kh, j, D, N, c->scale, c->mutation);
+                    Pi[j] = score(Qh + i * D, Kh, j, D, Nk, c->scale, c->mutation);
                 }
                 if (Pi[j] > m) m = Pi[j];
             }
             const double shift = (c->mutation == 5) ? 0.0 : m;
             double sum = 0.0;
-            for (i64 j = 0; j < N; ++j) {
+            for (i64 j = 0; j < Nk; ++j) {
                 Pi[j] = (Pi[j] == -INFINITY) ? 0.0 : exp(Pi[j] - shift);
                 sum += Pi[j];
             }
-            for (i64 j = 0; j < N; ++j) Pi[j] /= sum;
+            for (i64 j = 0; j < Nk; ++j) Pi[j] /= sum;
         }
-        /* dV = P^T dO */
-        for (i64 j = 0; j < N; ++j) {
+        /* dV = P^T dO (mutation 6 reads P transposed, defined for Nq == Nk only) */
+        for (i64 j = 0; j < Nk; ++j) {
             for (i64 d = 0; d < D; ++d) {
                 double s = 0.0;
-                for (i64 i = 0; i < N; ++i) {
-                    const double pij = (c->mutation == 6) ? P[j * N + i] : P[i * N + j];
+                for (i64 i = 0; i < Nq; ++i) {
+                    const double pij = (c->mutation == 6) ? P[j * Nk + i] : P[i * Nk + j];
                     s += pij * (double)dOh[i * D + d];
                 }
-                c->dV[off + j * D + d] = (float)s;
+                c->dV[koff + j * D + d] = (float)s;
             }
         }
         /* dP = dO V^T */
-        for (i64 i = 0; i < N; ++i)
-            for (i64 j = 0; j < N; ++j) {
+        for (i64 i = 0; i < Nq; ++i)
+            for (i64 j = 0; j < Nk; ++j) {
                 double s = 0.0;
                 for (i64 d = 0; d < D; ++d) s += (double)dOh[i * D + d] * (double)Vh[j * D + d];
-                dP[i * N + j] = s;
+                dP[i * Nk + j] = s;
             }
         /* dS = P (dP - D_i), D_i = sum_j P_ij dP_ij; stored in dP */
-        for (i64 i = 0; i < N; ++i) {
+        for (i64 i = 0; i < Nq; ++i) {
             double Di = 0.0;
-            for (i64 j = 0; j < N; ++j) Di += P[i * N + j] * dP[i * N + j];
-            for (i64 j = 0; j < N; ++j) {
-                if (masked_key(i, j, N, N, c->causal, c->mutation)) {
-                    dP[i * N + j] = 0.0;
+            for (i64 j = 0; j < Nk; ++j) Di += P[i * Nk + j] * dP[i * Nk + j];
+            for (i64 j = 0; j < Nk; ++j) {
+                if (masked_key(i, j, Nq, Nk, c->causal, c->mutation)) {
+                    dP[i * Nk + j] = 0.0;
                 } else {
-                    const double diff = (c->mutation == 3) ? dP[i * N + j] + Di : dP[i * N + j] - Di;
-                    dP[i * N + j] = P[i * N + j] * diff;
+                    const double diff =
+                        (c->mutation == 3) ? dP[i * Nk + j] + Di : dP[i * Nk + j] - Di;
+                    dP[i * Nk + j] = P[i * Nk + j] * diff;
                 }
             }
         }
         /* dQ = scale dS K, dK = scale dS^T Q */
-        for (i64 i = 0; i < N; ++i)
+        for (i64 i = 0; i < Nq; ++i)
             for (i64 d = 0; d < D; ++d) {
                 double s = 0.0;
-                for (i64 j = 0; j < N; ++j) s += dP[i * N + j] * (double)Kh[j * D + d];
-                c->dQ[off + i * D + d] = (float)(s * c->scale);
+                for (i64 j = 0; j < Nk; ++j) s += dP[i * Nk + j] * (double)Kh[j * D + d];
+                c->dQ[qoff + i * D + d] = (float)(s * c->scale);
             }
-        for (i64 j = 0; j < N; ++j)
+        for (i64 j = 0; j < Nk; ++j)
             for (i64 d = 0; d < D; ++d) {
                 double s = 0.0;
-                for (i64 i = 0; i < N; ++i) s += dP[i * N + j] * (double)Qh[i * D + d];
-                c->dK[off + j * D + d] = (float)(c->mutation == 4 ? s : s * c->scale);
+                for (i64 i = 0; i < Nq; ++i) s += dP[i * Nk + j] * (double)Qh[i * D + d];
+                c->dK[koff + j * D + d] = (float)(c->mutation == 4 ? s : s * c->scale);
             }
     }
     free(P);
@@ -246,10 +253,13 @@ static void bwd_heads(void* p, i64 begin, i64 end) {
 }
 
 int oracle_backward(const float* Q, const float* K, const float* V, const float* dO, float* dQ,
-                    float* dK, float* dV, i64 BH, i64 N, i64 D, double scale, int causal,
+                    float* dK, float* dV, i64 BH, i64 Nq, i64 Nk, i64 D, double scale, int causal,
                     int nthreads, int mutation) {
-    if (!Q || !K || !V || !dO || !dQ || !dK || !dV || BH <= 0 || N <= 0 || D <= 0) return 1;
-    bwd_ctx c = {Q, K, V, dO, dQ, dK, dV, N, D, scale, causal, mutation};
+    if (!Q || !K || !V || !dO || !dQ || !dK || !dV || BH <= 0 || Nq <= 0 || Nk <= 0 || D <= 0)
+        return 1;
+    if (causal && Nq > Nk) return 1; /* rows without any visible key */
+    if (mutation == 6 && Nq != Nk) return 1;
+    bwd_ctx c = {Q, K, V, dO, dQ, dK, dV, Nq, Nk, D, scale, causal, mutation};
     parallel_for(BH, nthreads, bwd_heads, &c);
     return 0;
 }

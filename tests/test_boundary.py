@@ -35,7 +35,7 @@ def test_library_loads_from_reference_search_path(lib):
 
 def test_every_declared_symbol_is_exported(lib):
     declared = _declared_c_symbols()
-    assert len(declared) == 19, declared
+    assert len(declared) == 25, declared
     out = subprocess.run(["nm", "-D", "--defined-only", lib.path], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
@@ -183,6 +183,48 @@ def test_decode_paged_validation(lib):
     assert call(d=16) == cuflash_attn.UNSUPPORTED_HEAD_DIM
     assert call(scale=math.inf) == cuflash_attn.INVALID_DIMENSION
     assert call(splits=-1) == cuflash_attn.INVALID_DIMENSION
+
+
+@pytest.mark.parametrize("sfx", ["f32", "f16", "bf16"])
+def test_ext_validation(lib, sfx):
+    """Extended forward / backward: the forward checks in order (null pointers, dimensions
+    including num_kv_heads and both lengths, head_dim in {32, 64, 96, 128, 256}, scale), then
+    the head grouping and, with a causal mask, q_len <= kv_len (DIMENSION_MISMATCH); the
+    backward checks its gradient pointers first. Every case returns before any GPU work."""
+    fwd = lib.fn("forward_ext", sfx)
+    bwd = lib.fn("backward_ext", sfx)
+    names = ["b", "h", "hkv", "nq", "nk", "d", "scale", "causal"]
+    ok = dict(b=1, h=8, hkv=2, nq=16, nk=40, d=96, scale=1.0, causal=True)
+
+    def f(ptrs=None, **kw):
+        a = dict(ok, **kw)
+        return fwd(*(ptrs or [P] * 5), *[a[n] for n in names], None)
+
+    def g(ptrs=None, **kw):
+        a = dict(ok, **kw)
+        return bwd(*(ptrs or [P] * 9), *[a[n] for n in names], None)
+
+    for call, n in ((f, 5), (g, 9)):
+        for i in range(n):
+            ptrs = [P] * n
+            ptrs[i] = None
+            assert call(ptrs) == cuflash_attn.NULL_POINTER
+        for dims in (dict(b=0), dict(h=-1), dict(hkv=0), dict(nq=0), dict(nk=-3), dict(d=0)):
+            assert call(**dims) == cuflash_attn.INVALID_DIMENSION
+        for d in (16, 48, 80, 160, 512):
+            assert call(d=d) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+        for scale in (math.nan, -1.0):
+            assert call(scale=scale) == cuflash_attn.INVALID_DIMENSION
+        assert call(hkv=3) == cuflash_attn.DIMENSION_MISMATCH
+        assert call(nq=41, nk=40) == cuflash_attn.DIMENSION_MISMATCH
+        # order: null before dims, dims before head_dim, head_dim before scale, scale before
+        # the grouping
+        assert call([None] + [P] * (n - 1), b=0) == cuflash_attn.NULL_POINTER
+        assert call(b=0, d=48) == cuflash_attn.INVALID_DIMENSION
+        assert call(d=48, scale=math.nan) == cuflash_attn.UNSUPPORTED_HEAD_DIM
+        assert call(scale=math.nan, hkv=3) == cuflash_attn.INVALID_DIMENSION
+    # q_len > kv_len is fine without a causal mask (checked up to the launch on the GPU tests)
+    assert g([P] * 5 + [None] + [P] * 3, b=-1) == cuflash_attn.NULL_POINTER
 
 
 def test_candidate_paths_follow_reference_order(monkeypatch):

@@ -273,6 +273,75 @@ def test_naive_fp32_baseline_agrees():
 
 
 # ------------------------------------------------------------------------------------------
+# separate query / key lengths (Q [B,H,Nq,D], K/V [B,H,Nk,D]; causal: j <= i + Nk - Nq)
+# ------------------------------------------------------------------------------------------
+def torch_attention_f64(q, k, v, do, scale, causal):
+    """O, L, dQ, dK, dV of softmax(scale Q K^T + mask) V in float64 on the CPU (torch autograd),
+    the mask written out as an explicit bottom-right aligned causal mask."""
+    import torch
+
+    tq, tk, tv = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v))
+    s = torch.matmul(tq, tk.transpose(-1, -2)) * scale
+    if causal:
+        nq, nk = q.shape[2], k.shape[2]
+        i = torch.arange(nq)[:, None]
+        j = torch.arange(nk)[None, :]
+        s = s.masked_fill(j > i + (nk - nq), float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    o = torch.matmul(torch.softmax(s, dim=-1), tv)
+    o.backward(torch.tensor(do, dtype=torch.float64))
+    return [t.detach().numpy() for t in (o, lse, tq.grad, tk.grad, tv.grad)]
+
+
+SEPARATE_LENGTHS = [(5, 37, True), (5, 37, False), (33, 100, True), (64, 71, True),
+                    (40, 17, False), (1, 9, True)]
+
+
+@pytest.mark.parametrize("nq,nk,causal", SEPARATE_LENGTHS)
+def test_separate_lengths_match_torch_float64(nq, nk, causal):
+    d = 32
+    q, do = rand(70, (2, 2, nq, d)), rand(71, (2, 2, nq, d))
+    k, v = rand(72, (2, 2, nk, d)), rand(73, (2, 2, nk, d))
+    scale = d ** -0.5
+    o_ref, l_ref, dq_ref, dk_ref, dv_ref = torch_attention_f64(q, k, v, do, scale, causal)
+    o, lse = oracle.forward(q, k, v, scale, causal)
+    np.testing.assert_allclose(o, o_ref, atol=2e-6)
+    np.testing.assert_allclose(lse, l_ref, atol=2e-6)
+    dq, dk, dv = oracle.backward(q, k, v, do, scale, causal)
+    for got, ref in ((dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        np.testing.assert_allclose(got, ref, atol=5e-6)
+
+
+def suffix_identity_fails(mutation=0) -> bool:
+    """Queries that are the last nq rows of an n-row sequence, attending causally to all n keys,
+    give the last nq rows of the full causal attention; with dO = 0 on the first n - nq rows the
+    full problem's dK, dV and last dQ rows are the gradients of the short one."""
+    n, nq, d = 50, 13, 32
+    q, k, v, do = (rand(80 + i, (1, 2, n, d)) for i in range(4))
+    do[:, :, : n - nq] = 0.0
+    scale = d ** -0.5
+    o_full, l_full = oracle.forward(q, k, v, scale, True)
+    o, lse = oracle.forward(q[:, :, n - nq:], k, v, scale, True, mutation=mutation)
+    if not (np.allclose(o, o_full[:, :, n - nq:], atol=1e-6)
+            and np.allclose(lse, l_full[:, :, n - nq:], atol=1e-6)):
+        return True
+    dq_full, dk_full, dv_full = oracle.backward(q, k, v, do, scale, True)
+    dq, dk, dv = oracle.backward(q[:, :, n - nq:], k, v, do[:, :, n - nq:], scale, True,
+                                 mutation=mutation)
+    return not (np.allclose(dq, dq_full[:, :, n - nq:], atol=1e-6)
+                and np.allclose(dk, dk_full, atol=1e-6) and np.allclose(dv, dv_full, atol=1e-6))
+
+
+def test_suffix_queries_equal_rows_of_full_causal_attention():
+    assert not suffix_identity_fails()
+
+
+def test_separate_length_checks_catch_top_left_mask():
+    assert suffix_identity_fails(7)
+    assert not golden_fails(7)  # square heads cannot tell the two alignments apart
+
+
+# ------------------------------------------------------------------------------------------
 # mutation tests: every planted mistake is caught by at least one of the checks above
 # ------------------------------------------------------------------------------------------
 def golden_fails(mutation) -> bool:
