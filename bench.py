@@ -20,8 +20,11 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
   tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
   timed on a bounded sample of the config-3 workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-decode]
-                      [--no-ext]
+Before the W warmup steps the step runs untimed for --ramp-ms (default 1 s): the first few dozen
+steps after the inputs are written run 5-10% slower while the GPU's clock settles.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu-baseline]
+                      [--no-decode] [--no-ext]
 """
 
 from __future__ import annotations
@@ -105,6 +108,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ramp-ms", type=float, default=1000.0,
+                    help="untimed steps for at least this long before the warmup steps, so that "
+                         "the GPU reaches its steady clock (default 1000 ms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -250,7 +256,16 @@ def main():
         if st != 0:
             raise RuntimeError(f"library status {st}")
 
-    log(f"warmup {args.warmup}")
+    # Steady state first: the first few dozen steps after the inputs are generated run 5-10%
+    # slower (clock and power ramp), which no fixed small warmup count covers.
+    log(f"ramp {args.ramp_ms:.0f} ms, then warmup {args.warmup}")
+    ramp_steps = 0
+    r0 = time.perf_counter()
+    while (time.perf_counter() - r0) * 1e3 < args.ramp_ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        ramp_steps += 10
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -482,6 +497,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "ramp": {"ms": args.ramp_ms, "steps": ramp_steps},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

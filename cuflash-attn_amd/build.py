@@ -29,7 +29,7 @@ BUILD_DIR = os.path.join(REPO_ROOT, "build")
 LIB_NAME = "libcuflash_attn.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
 
-SOURCES = ["api.cpp", "profile.cpp", "forward.hip", "backward.hip", "decode.hip",
+SOURCES = ["api.cpp", "profile.cpp", "workspace.cpp", "forward.hip", "backward.hip", "decode.hip",
            "primitives.hip"]
 # C++ test programs linked against the library (sources under tests/cpp, binaries in build/).
 TEST_PROGRAMS = {"test_primitives": "test_primitives.cpp"}

@@ -71,8 +71,14 @@ inline FlashAttentionError from_hip(hipError_t e) {
     return FlashAttentionError::CUDA_ERROR;
 }
 
-// Stream-ordered device workspace (hipMallocAsync / hipFreeAsync on the caller's stream), the
-// counterpart of the reference's AsyncFloatBuffer (src/backward/flash_attention_backward_typed.cu
+// The library's own stream-ordered memory pool on the current device (created on first use,
+// kept until the process ends, release threshold at its maximum so that freed blocks stay in the
+// pool and later allocations of the same size need no driver call). Using a private pool leaves
+// the application's default pool and its settings untouched. nullptr when it cannot be created.
+hipMemPool_t workspace_pool();
+
+// Stream-ordered device workspace (hipMallocFromPoolAsync / hipFreeAsync on the caller's stream),
+// the counterpart of the reference's AsyncFloatBuffer (src/backward/flash_attention_backward_typed.cu
 // :374-394). Freed in stream order when the launcher returns, so the host never synchronizes and
 // concurrent calls on different streams never share memory.
 class StreamWorkspace {
@@ -84,7 +90,9 @@ public:
         if (ptr_) (void)hipFreeAsync(ptr_, stream_);
     }
     FlashAttentionError alloc(size_t bytes) {
-        hipError_t e = hipMallocAsync(&ptr_, bytes, stream_);
+        hipMemPool_t pool = workspace_pool();
+        hipError_t e = pool ? hipMallocFromPoolAsync(&ptr_, bytes, pool, stream_)
+                            : hipMallocAsync(&ptr_, bytes, stream_);
         if (e != hipSuccess) {
             ptr_ = nullptr;
             (void)hipGetLastError();

@@ -1,0 +1,52 @@
+// Library-owned stream-ordered memory pools for the launchers' workspaces (one per device).
+//
+// hipMallocAsync from a pool whose release threshold is 0 (the default) hands freed memory back
+// at every synchronization, so each call's workspace needs fresh driver work. A private pool per
+// device with the threshold at its maximum keeps the few MiB the launchers use (the backward's
+// row statistics, the decode partials) cached, and leaves the application's pools alone.
+
+#include <cstdint>
+#include <mutex>
+
+#include "launch.hpp"
+
+namespace cuflash {
+namespace detail {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_pool_mutex;
+hipMemPool_t g_pools[kMaxDevices] = {};
+bool g_tried[kMaxDevices] = {};
+}  // namespace
+
+hipMemPool_t workspace_pool() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    if (!g_tried[dev]) {
+        g_tried[dev] = true;
+        hipMemPoolProps props = {};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
+            uint64_t keep = UINT64_MAX;
+            if (hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) == hipSuccess) {
+                g_pools[dev] = pool;
+            } else {
+                (void)hipMemPoolDestroy(pool);
+            }
+        }
+        (void)hipGetLastError();
+    }
+    return g_pools[dev];
+}
+
+}  // namespace detail
+}  // namespace cuflash
