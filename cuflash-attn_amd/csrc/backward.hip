@@ -31,6 +31,7 @@
 #include "launch.hpp"
 #include "profile.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace cuflash {
@@ -456,13 +457,15 @@ __global__ void __launch_bounds__(256, 1)
 // ------------------------------------------------------------------------------------------
 // Row statistics for the D = 128 kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
-// without any masking. N is the query length.
+// without any masking. N is the query length. Block 0 also clears the kNumXcd work-queue
+// counters of the bwd_d128_kernel launch that follows on the stream.
 template <typename T>
 __global__ void __launch_bounds__(256)
     delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
                     const float* __restrict__ L, float2* __restrict__ LD, int N, int Npad,
-                    long long rows_pad) {
+                    long long rows_pad, int* __restrict__ queues) {
     constexpr int D = 128;
+    if (blockIdx.x == 0 && threadIdx.x < kNumXcd) queues[threadIdx.x] = 0;
     constexpr int LPR = D / 8;  // lanes per row
     const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     const long long prow = t / LPR;  // padded row index
@@ -869,12 +872,21 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
     }
 }
 
-// One launch for both passes (they are independent once delta_ld_kernel has run): workgroup
-// ids alternate between the dq and the dkdv grid, each in its own longest-first order, so the
-// two halves share the machine and their tails overlap instead of adding a kernel boundary.
-// The grid holds BH * nqb dq workgroups (128 query rows each) and BHkv * nkb dkdv workgroups
-// (128 keys each); when the counts differ, the ids past twice the smaller one run the rest of
-// the larger grid.
+// One launch for both passes (they are independent once delta_ld_kernel has run), as a pool
+// of resident workgroups that take work items from kNumXcd queues. Queue x belongs to XCD x:
+// even XCDs take the dkdv items (128 keys each, BHkv * nkb of them), odd XCDs the dq items
+// (128 query rows each, BH * nqb), each XCD the ids congruent to x / 2 modulo 4, in increasing
+// order: every XCD keeps its own heads (their tiles stay in its L2) and runs its longest items
+// first. A workgroup whose own queue is empty takes from the next XCD's queue, then from the
+// others, and exits when every queue is empty. The dq items need about 70% of the dkdv items'
+// time, so without the hand-over the dq XCDs would idle for the last third of the launch.
+// Counters are cleared by delta_ld_kernel; every workgroup ends after at most one failed pass
+// over the queues, so the launch always drains.
+__device__ __forceinline__ int xcc_id() {
+    return static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20)) &
+           (kNumXcd - 1);  // HW_REG_XCC_ID[3:0]
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256, 2)
     bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -882,31 +894,42 @@ __global__ void __launch_bounds__(256, 2)
                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
                     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int Nq, int Nk,
                     int coff, int group, int Npad, int nqb, int nkb, int BH, float c,
-                    float scale, int causal) {
+                    float scale, int causal, int* __restrict__ queues) {
     constexpr int kLds = kDkdvLds > kDqLds ? kDkdvLds : kDqLds;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
+    __shared__ int item;
     const int BHkv = BH / group;
     const int n_dq = BH * nqb;
     const int n_dkdv = BHkv * nkb;
-    const int both = min(n_dq, n_dkdv);
-    const int bid = blockIdx.x;
-    bool is_dq;
-    int id;
-    if (bid < 2 * both) {  // interleaved part
-        is_dq = (bid & 1) != 0;
-        id = bid >> 1;
-    } else {
-        is_dq = n_dq > n_dkdv;
-        id = bid - both;
-    }
-    if (is_dq) {
-        if (id < n_dq)
+    const int home = xcc_id();
+    for (;;) {
+        if (threadIdx.x == 0) {
+            int got = -1;
+            for (int t = 0; t < kNumXcd && got < 0; ++t) {
+                const int qx = (home + t) & (kNumXcd - 1);
+                const int j = qx >> 1;
+                const int n = (qx & 1) ? n_dq : n_dkdv;
+                const int len = n > j ? (n - j + 3) / 4 : 0;  // ids j, j + 4, ... below n
+                if (__hip_atomic_load(&queues[qx], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) >= len)
+                    continue;  // empty: no read-modify-write on a drained counter
+                const int k = atomicAdd(&queues[qx], 1);
+                if (k < len) got = ((qx & 1) << 30) | (4 * k + j);
+            }
+            item = got;
+        }
+        __syncthreads();
+        const int it = item;
+        __syncthreads();  // every wave has read `item` before thread 0 writes the next one
+        if (it < 0) break;
+        const int id = it & ((1 << 30) - 1);
+        if (it >> 30)
             dq_d128<T>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
                        causal, id, smem);
-    } else {
-        if (id < n_dkdv)
+        else
             dkdv_d128<T>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad, BHkv, c, scale,
                          causal, id, smem);
+        __syncthreads();  // the next item reuses the LDS tiles
     }
 }
 
@@ -997,9 +1020,12 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     const int Npad = (sh.Nq + 31) / 32 * 32;
     const long long rows_pad = static_cast<long long>(sh.BH) * Npad;
     StreamWorkspace ws(stream);
-    FlashAttentionError err = ws.alloc(static_cast<size_t>(rows_pad) * sizeof(float2));
+    // (L log2 e, D) rows, then the kNumXcd work-queue counters of bwd_d128_kernel
+    const size_t ld_bytes = static_cast<size_t>(rows_pad) * sizeof(float2);
+    FlashAttentionError err = ws.alloc(ld_bytes + dev::kNumXcd * sizeof(int));
     if (err != FlashAttentionError::SUCCESS) return err;
     float2* ld = static_cast<float2*>(ws.get());
+    int* queues = reinterpret_cast<int*>(static_cast<unsigned char*>(ws.get()) + ld_bytes);
 
     const long long dblocks = (rows_pad * (D / 8) + 255) / 256;
     const int nqb = (sh.Nq + 127) / 128;
@@ -1017,17 +1043,19 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     int tok = profile_kernel<T, D>("backward_delta", stream);
     hipLaunchKernelGGL((dev::delta_ld_kernel<T>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, sh.Nq, Npad,
-                       rows_pad);
+                       rows_pad, queues);
     profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
+    // Two resident workgroups per CU take the qblocks + kblocks work items.
+    const long long pool = std::min<long long>(qblocks + kblocks, 2LL * compute_units());
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
-    hipLaunchKernelGGL((dev::bwd_d128_kernel<T>), dim3(static_cast<unsigned>(qblocks + kblocks)),
-                       dim3(256), 0, stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ),
+    hipLaunchKernelGGL((dev::bwd_d128_kernel<T>), dim3(static_cast<unsigned>(pool)), dim3(256), 0,
+                       stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ),
                        reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), sh.Nq,
                        sh.Nk, sh.Nk - sh.Nq, sh.group, Npad, nqb, nkb, sh.BH, c, scale,
-                       causal ? 1 : 0);
+                       causal ? 1 : 0, queues);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }

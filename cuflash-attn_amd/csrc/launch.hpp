@@ -71,6 +71,9 @@ inline FlashAttentionError from_hip(hipError_t e) {
     return FlashAttentionError::CUDA_ERROR;
 }
 
+// Compute units of the current device (cached per device; 256 on MI355X when the query fails).
+int compute_units();
+
 // The library's own stream-ordered memory pool on the current device (created on first use,
 // kept until the process ends, release threshold at its maximum so that freed blocks stay in the
 // pool and later allocations of the same size need no driver call). Using a private pool leaves
