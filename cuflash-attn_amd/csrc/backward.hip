@@ -601,7 +601,6 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         const int q0 = (qb_begin + it % span) * BM;
         __builtin_amdgcn_s_waitcnt(0);  // block it is in LDS
         __syncthreads();                // ... for every wave; block it - 1 is no longer read
-        if (it + 1 < n_it) load_block(it + 1, b ^ 1);
         const unsigned char* qt = smem + b * SET;
         const unsigned char* ot = qt + QT;
         const float2* ldv = reinterpret_cast<const float2*>(qt + 2 * QT);
@@ -638,6 +637,11 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
             for (int r = 0; r < 16; ++r)
                 s[r] = (8 * (r >> 2) + (r & 3) < lim) ? -INFINITY : s[r];
         }
+        // Next block's tile loads. Issued here, after the S / dP MFMAs: a load waits at issue
+        // while the CU's vector memory path drains the other waves' loads, and here that wait
+        // overlaps the MFMAs in flight; before them it delays the MFMAs, after the P / dS
+        // arithmetic it delays the dV / dK MFMAs (both measured slower).
+        if (it + 1 < n_it) load_block(it + 1, b ^ 1);
         frag bp[2], bs[2];
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
