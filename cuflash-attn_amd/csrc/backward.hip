@@ -507,10 +507,14 @@ __device__ __forceinline__ int grp_tr_sub() {  // transpose reads, without the r
     return (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 + (kq & 1) * 8;
 }
 
-// Key-stationary part of workgroup `bid` of BHkv * nkb (kb = 0, the most work, first); smem
-// holds at least kDkdvLds bytes.
+// Key-stationary part of work item `bid` of heads * nkb (kb = 0, the most work, first); smem
+// holds at least kDkdvLds bytes. Without kShares an item is (key/value head, key block) and runs
+// over all `group` query heads of its key/value head (heads = BHkv), storing dK, dV. With
+// kShares an item is (query head, key block) (heads = BH): it runs over that query head only
+// and stores its fp32 share of dK (scaled) and dV at part[bh] and part[BH + bh] ([BH, Nk, D]
+// each), which dkdv_reduce_kernel sums over each group.
 constexpr int kDkdvLds = 2 * (2 * 8 * kGrp128 + 32 * 8);
-template <typename T>
+template <typename T, bool kShares>
 __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                                           const uint16_t* __restrict__ K,
                                           const uint16_t* __restrict__ V,
@@ -518,8 +522,8 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                                           const uint16_t* __restrict__ dO,
                                           uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
                                           int Nq, int Nk, int coff, int group, int Npad,
-                                          int BHkv, float c, float scale, int causal, int bid,
-                                          unsigned char* smem) {
+                                          int heads, float c, float scale, int causal, int bid,
+                                          unsigned char* smem, float* __restrict__ part) {
     constexpr int D = 128;
     constexpr int BN = 128;  // keys per workgroup (32 per wave)
     constexpr int BM = 32;   // query rows per block
@@ -529,8 +533,11 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
     static_assert(2 * SET == kDkdvLds, "LDS size");
     using frag = typename Elem<T>::frag;
 
-    int bkv, kb;  // key/value head, key block
-    head_rank_order(bid, BHkv, bkv, kb);
+    int hi, kb;  // item head, key block
+    head_rank_order(bid, heads, hi, kb);
+    const int bkv = kShares ? hi / group : hi;    // key/value head
+    const int bq0 = kShares ? hi : hi * group;    // first query head of the item
+    const int qheads = kShares ? 1 : group;       // query heads of the item
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31;
@@ -555,19 +562,19 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         vf[ks] = as_frag<T>(vv);
     }
 
-    // Query blocks [qb_begin, nqb) of each of the `group` query heads of this key/value head, as
-    // one sequence of n_it iterations (it -> head bkv * group + it / span, block
-    // qb_begin + it % span); with a causal mask the blocks before the first query that sees key
-    // kwg are skipped. qb_begin < nqb because that query is below Nq.
+    // Query blocks [qb_begin, nqb) of each query head of the item, as one sequence of n_it
+    // iterations (it -> head bq0 + it / span, block qb_begin + it % span); with a causal mask
+    // the blocks before the first query that sees key kwg are skipped. qb_begin < nqb because
+    // that query is below Nq.
     const int nqb = Npad / BM;
     const int qb_begin = causal ? max(0, kwg - coff) / BM : 0;
     const int span = nqb - qb_begin;
-    const int n_it = group * span;
+    const int n_it = qheads * span;
 
     const int ld_row = lane & 3;
     const int ld_col = (lane >> 2) * 8;
     auto load_block = [&](int it, int b) {
-        const int bh = bkv * group + it / span;
+        const int bh = bq0 + it / span;
         const int r0 = (qb_begin + it % span) * BM;
         const size_t q_head = static_cast<size_t>(bh) * Nq * D;
         const uint16_t* Qh = Q + q_head;
@@ -692,7 +699,25 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         }
     }
 
-    if (key_ok) {
+    if (kShares && key_ok) {
+        float* krow = part + (static_cast<size_t>(hi) * Nk + key) * D;
+        float* vrow = part + (static_cast<size_t>(heads + hi) * Nk + key) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int d = 32 * dt + 8 * a + 4 * g2;
+                f32x4 wk, wv;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    wk[u] = dk[dt][4 * a + u] * scale;
+                    wv[u] = dv[dt][4 * a + u];
+                }
+                st16(krow + d, __builtin_bit_cast(u32x4, wk));
+                st16(vrow + d, __builtin_bit_cast(u32x4, wv));
+            }
+        }
+    } else if (!kShares && key_ok) {
         uint16_t* krow = dK + kv_head + static_cast<size_t>(key) * D;
         uint16_t* vrow = dV + kv_head + static_cast<size_t>(key) * D;
 #pragma unroll
@@ -891,20 +916,20 @@ __device__ __forceinline__ int xcc_id() {
            (kNumXcd - 1);  // HW_REG_XCC_ID[3:0]
 }
 
-template <typename T>
+template <typename T, bool kShares>
 __global__ void __launch_bounds__(256, 2)
     bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
                     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int Nq, int Nk,
                     int coff, int group, int Npad, int nqb, int nkb, int BH, float c,
-                    float scale, int causal, int* __restrict__ queues) {
+                    float scale, int causal, int* __restrict__ queues, float* __restrict__ part) {
     constexpr int kLds = kDkdvLds > kDqLds ? kDkdvLds : kDqLds;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
     __shared__ int item;
-    const int BHkv = BH / group;
+    const int dkdv_heads = kShares ? BH : BH / group;  // see dkdv_d128
     const int n_dq = BH * nqb;
-    const int n_dkdv = BHkv * nkb;
+    const int n_dkdv = dkdv_heads * nkb;
     const int home = xcc_id();
     for (;;) {
         if (threadIdx.x == 0) {
@@ -931,9 +956,40 @@ __global__ void __launch_bounds__(256, 2)
             dq_d128<T>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
                        causal, id, smem);
         else
-            dkdv_d128<T>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad, BHkv, c, scale,
-                         causal, id, smem);
+            dkdv_d128<T, kShares>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad,
+                                  dkdv_heads, c, scale, causal, id, smem, part);
         __syncthreads();  // the next item reuses the LDS tiles
+    }
+}
+
+// dK, dV of each key/value head from the fp32 shares of its `group` query heads (the
+// part != nullptr mode of dkdv_d128): part holds dK shares [BH, Nk, D], then dV shares. Eight
+// elements per thread; sums in fp32 in head order, one rounding to T.
+template <typename T>
+__global__ void __launch_bounds__(256)
+    dkdv_reduce_kernel(const float* __restrict__ part, uint16_t* __restrict__ dK,
+                       uint16_t* __restrict__ dV, long long kv_elems, long long head_elems,
+                       int group) {
+    const long long e = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (e >= kv_elems) return;
+    const long long bkv = e / head_elems;
+    const long long off = e - bkv * head_elems;
+    const long long q_elems = kv_elems * group;  // BH * Nk * D
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        const float* src = part + which * q_elems + (bkv * group) * head_elems + off;
+        f32x4 a = __builtin_bit_cast(f32x4, ld16(src));
+        f32x4 b = __builtin_bit_cast(f32x4, ld16(src + 4));
+        for (int g = 1; g < group; ++g) {
+            a += __builtin_bit_cast(f32x4, ld16(src + g * head_elems));
+            b += __builtin_bit_cast(f32x4, ld16(src + g * head_elems + 4));
+        }
+        u32x4 w;
+        w[0] = Elem<T>::pack2(a[0], a[1]);
+        w[1] = Elem<T>::pack2(a[2], a[3]);
+        w[2] = Elem<T>::pack2(b[0], b[1]);
+        w[3] = Elem<T>::pack2(b[2], b[3]);
+        st16((which ? dV : dK) + e, w);
     }
 }
 
@@ -1034,8 +1090,14 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     const long long dblocks = (rows_pad * (D / 8) + 255) / 256;
     const int nqb = (sh.Nq + 127) / 128;
     const int nkb = (sh.Nk + 127) / 128;
+    // Grouped heads: one dkdv item per (query head, key block) with fp32 shares of dK, dV that a
+    // second kernel sums, when the shares fit in kMaxShareBytes; an item per (key/value head,
+    // key block) would run `group` times longer and leave the launch's tail to a few of them.
+    constexpr long long kMaxShareBytes = 2LL << 30;
+    const long long share_bytes = 2LL * sh.BH * sh.Nk * D * static_cast<long long>(sizeof(float));
+    const bool shares = sh.group > 1 && share_bytes <= kMaxShareBytes;
     const long long qblocks = static_cast<long long>(nqb) * sh.BH;
-    const long long kblocks = static_cast<long long>(nkb) * (sh.BH / sh.group);
+    const long long kblocks = static_cast<long long>(nkb) * (shares ? sh.BH : sh.BH / sh.group);
     if (dblocks > 0x7fffffffLL || qblocks + kblocks > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
     const float c = scale * dev::kLog2e;
@@ -1052,14 +1114,33 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
+    StreamWorkspace share_ws(stream);
+    float* part = nullptr;
+    if (shares) {
+        err = share_ws.alloc(static_cast<size_t>(share_bytes));
+        if (err != FlashAttentionError::SUCCESS) return err;
+        part = static_cast<float*>(share_ws.get());
+    }
+
     // Two resident workgroups per CU take the qblocks + kblocks work items.
     const long long pool = std::min<long long>(qblocks + kblocks, 2LL * compute_units());
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
-    hipLaunchKernelGGL((dev::bwd_d128_kernel<T>), dim3(static_cast<unsigned>(pool)), dim3(256), 0,
-                       stream, q, k, v, ld, go, reinterpret_cast<uint16_t*>(dQ),
-                       reinterpret_cast<uint16_t*>(dK), reinterpret_cast<uint16_t*>(dV), sh.Nq,
-                       sh.Nk, sh.Nk - sh.Nq, sh.group, Npad, nqb, nkb, sh.BH, c, scale,
-                       causal ? 1 : 0, queues);
+    auto kernel = shares ? dev::bwd_d128_kernel<T, true> : dev::bwd_d128_kernel<T, false>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
+                       ld, go, reinterpret_cast<uint16_t*>(dQ), reinterpret_cast<uint16_t*>(dK),
+                       reinterpret_cast<uint16_t*>(dV), sh.Nq, sh.Nk, sh.Nk - sh.Nq, sh.group,
+                       Npad, nqb, nkb, sh.BH, c, scale, causal ? 1 : 0, queues, part);
+    profile_end(tok, stream);
+    err = from_hip(hipGetLastError());
+    if (err != FlashAttentionError::SUCCESS || !shares) return err;
+
+    const long long kv_elems = static_cast<long long>(sh.BH / sh.group) * sh.Nk * D;
+    const long long rblocks = (kv_elems / 8 + 255) / 256;
+    tok = profile_kernel<T, D>("backward_dkdv_reduce", stream);
+    hipLaunchKernelGGL((dev::dkdv_reduce_kernel<T>), dim3(static_cast<unsigned>(rblocks)),
+                       dim3(256), 0, stream, part, reinterpret_cast<uint16_t*>(dK),
+                       reinterpret_cast<uint16_t*>(dV), kv_elems,
+                       static_cast<long long>(sh.Nk) * D, sh.group);
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
