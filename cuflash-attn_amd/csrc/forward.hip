@@ -8,6 +8,8 @@
 //                       reference WMMA kernel (forward_wmma.cu:151-156).
 //   fwd32_kernel<D>:    fp32 inputs on v_mfma_f32_32x32x2f32 (full fp32 products), P kept fp32
 //                       as in the reference scalar kernel (forward_typed.cu:113-129).
+// fp16 / bf16 at head_dim 128 and 64 run the software-pipelined fwd16_d128_kernel and
+// fwd16_d64_kernel (same math, LDS-DMA tiles; described at their definitions).
 //
 // Work decomposition (both kernels): one workgroup = 4 waves = 128 query rows of one
 // (batch, head); each wave owns 32 query rows. The kernel streams key/value blocks through LDS;
@@ -517,6 +519,315 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 }
 
 // ------------------------------------------------------------------------------------------
+// fp16 / bf16 kernel for head_dim 64
+// ------------------------------------------------------------------------------------------
+// fwd16_d128_kernel's data path and pipeline at head_dim 64 (config 2's shape): 64-key blocks
+// in LDS-DMA double buffers, one workgroup of NW waves per CU, the next block's scores formed
+// while the current block's softmax runs. A 64-element row is 128 bytes, so one load
+// instruction (64 lanes x 16 bytes) fills a group of 8 rows; the group layout is given at the
+// operand offsets below.
+template <typename T, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW)
+    fwd16_d64_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                      const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
+                      float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
+                      float c, int causal) {
+    constexpr int D = 64;
+    constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
+    constexpr int BN = 64;
+    constexpr int kParts = 8 / NW;  // load instructions per wave per 64-row tile
+    constexpr int GRP = 1152;              // bytes per 8-row group
+    constexpr int TILE = (BN / 8) * GRP;   // bytes per 64-row tile
+    static_assert(kParts >= 1, "at most eight waves");
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
+
+    int bh, rank;
+    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
+    const int q0 = qb * BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;              // query row owned by this lane
+
+    frag qf[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < Nq) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    const int kv_end = causal ? min(Nk, (qb + 1) * BM + coff) : Nk;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    // Loads of one 64-row tile: wave w fills groups w, w + NW, ... (kParts of them), one
+    // 8-row group (1 KB) per load instruction: lane i writes slot i, i.e. chunk i / 8 of row
+    // (i % 8) ^ (4 ((i >> 4) & 1)) of the group. Rows past Nk are clamped to row Nk - 1 (finite
+    // values; their scores are masked). Issued from inline assembly as in fwd16_d128_kernel.
+    // A tile that lies inside [0, Nk) is addressed as a scalar base plus a fixed per-lane offset.
+    const int ld_row = (lane & 7) ^ (4 * ((lane >> 4) & 1));
+    const int ld_col = (lane >> 3) * 8;
+    const unsigned ld_voff = static_cast<unsigned>(((8 * wave + ld_row) * D + ld_col) * 2);
+    // Part i (0..kParts-1) of a tile load: this wave's group wave + NW i.
+    auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
+        if (key0 + BN <= Nk) {
+            lds_dma16_async_s(src + static_cast<size_t>(key0 + 8 * NW * i) * D, ld_voff,
+                              dst + (wave + NW * i) * GRP);
+        } else {
+            const int grp = wave + NW * i;
+            const int row = min(key0 + 8 * grp + ld_row, Nk - 1);
+            lds_dma16_async(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
+        }
+    };
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+#pragma unroll
+        for (int i = 0; i < kParts; ++i) load_part(src, key0, dst, i);
+    };
+    // Per-lane byte offsets of the operand reads. Chunk c of row r of a group sits at
+    // 16 (8 c + (r ^ 4 ((c >> 1) & 1))): 16 rows of one chunk (K row reads) fall on 16 distinct
+    // 16-byte bank slots (the 128 bytes of padding per group shift the next 8 rows by 8 slots),
+    // and the 32 lanes of a V transpose read (4 rows x 8 chunk halves) on 32 distinct 8-byte
+    // slots (the row swizzle moves the chunks 2-3 of a 64-byte span to the other rows).
+    // K row reads: chunk 2 ks + g2, so the swizzle bit is ks & 1.
+    const int k_off_even = (l32 >> 3) * GRP + g2 * 128 + (l32 & 7) * 16;
+    const int k_off_odd = (l32 >> 3) * GRP + g2 * 128 + ((l32 & 7) ^ 4) * 16;
+    const int kq = lane & 15;
+    const int gl = (lane >> 4) & 1;
+    const int v_off = (2 * gl + ((kq & 3) >> 1)) * 128 + (g2 ^ gl) * 64 + (kq >> 2) * 16 +
+                      (kq & 1) * 8;
+    auto k_addr = [&](const unsigned char* kt, int t, int ks) {
+        return kt + ((ks & 1) ? k_off_odd : k_off_even) + 4 * t * GRP + ks * 256;
+    };
+
+    auto scores = [&](const unsigned char* kt, f32x16 (&s)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks)
+                s[t] = Elem<T>::mma(as_frag<T>(ld16(k_addr(kt, t, ks))), qf[ks], s[t]);
+        }
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;  // running max of s * cs (log2 units)
+    float l = 0.0f;       // this lane's share of the running row sum
+    // Exponent scale, kept positive so that a masked score (-inf) always maps to p = 0, also
+    // for scale = 0 (where FLT_MIN leaves every p at 1 and L at log(count), as with 0).
+    const float cs = fmaxf(c, kFltMin);
+
+    // Keys past Nk and, with a causal mask, keys after this lane's row get s = -inf.
+    auto mask_scores = [&](f32x16 (&s)[2], int key0) {
+        const int lim = min(Nk, causal ? q + 1 + coff : Nk) - key0 - 4 * g2;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 32 * t + 8 * (r >> 2) + (r & 3);
+                s[t][r] = off < lim ? s[t][r] : -INFINITY;
+            }
+        }
+    };
+
+    // Online-softmax update of (m, l) from mx, this lane's raw row max of the next block.
+    // Returns whether some lane of the wave must rescale its O by alpha. The lazy rescale is
+    // decided per lane with selects: m only moves when the block max exceeds it by more than
+    // kLazyRescale, and O and l of that lane are scaled by the same alpha, so the result is
+    // exact either way.
+    auto update_max = [&](float mx, float& alpha) -> bool {
+        const float m_new = fmaxf(m, pair_max(mx) * cs);
+        const bool grow = m_new > m + kLazyRescale;
+        const float a_raw = fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new);
+        alpha = grow ? a_raw : 1.0f;
+        m = grow ? m_new : m;
+        l *= alpha;
+        return __ballot(grow) != 0;
+    };
+
+    // Operand fragment i of the score MFMAs (K rows of tile half i / 4, k-step i % 4) and of
+    // the P V MFMAs (V^T for key group i / 2 and d tile i % 2).
+    auto k_frag = [&](const unsigned char* kt, int i) {
+        return as_frag<T>(ld16(k_addr(kt, i >> 2, i & 3)));
+    };
+    auto v_frag = [&](const unsigned char* vt, int i) {
+        const unsigned char* a0 = vt + v_off + 2 * (i >> 1) * GRP + (i & 1) * 512;
+        return tr_frag_at<T>(a0, a0 + GRP);
+    };
+
+    // Blocks that need masking: keys past Nk, and with a causal mask the blocks that reach past
+    // the last key this wave's first row sees.
+    auto needs_mask = [&](int key0) {
+        return key0 + BN > Nk || (causal && key0 + BN - 1 > q0 + coff);
+    };
+
+    // Exponential of score r of tile t, and the rounding of tile t's group h of eight scores
+    // to T (the P operand of key group 2 t + h).
+    auto exp_one = [&](f32x16 (&s)[2], int t, int r, float m_use) {
+        s[t][r] = fast_exp2(fmaf(s[t][r], cs, -m_use));
+    };
+    auto pack_p = [&](f32x16 (&s)[2], int t, int h) {
+        u32x4 pw = __builtin_bit_cast(
+            u32x4, pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2],
+                                s[t][8 * h + 3], s[t][8 * h + 4], s[t][8 * h + 5],
+                                s[t][8 * h + 6], s[t][8 * h + 7]));
+        // Keep the exponentials where they are placed: left alone, the compiler sinks them
+        // to their first use past the branches in between.
+        asm volatile("" : "+v"(pw));
+        return __builtin_bit_cast(frag, pw);
+    };
+
+    // One block with an explicit instruction order (the scheduling fences keep it), as in
+    // fwd16_d128_kernel with half the MFMAs per phase (the softmax work per key is the same, so
+    // every MFMA carries twice the VALU work):
+    //   phase A: the 8 MFMAs of the next block's scores into s_next, each with the exponentials
+    //            of two scores of the current tile 0 (P groups 0 and 1); the wave's K load part
+    //            after MFMA 1, its V load part after MFMA 5;
+    //   phase B: the 8 MFMAs of O^T += V^T P^T; MFMAs 0-3 carry the exponentials of tile 1
+    //            (P groups 2 and 3, first used by MFMAs 4 and 6), every MFMA four terms of the
+    //            fp32 row sum and the max of four scores of s_next.
+    // Returns this lane's raw row max of s_next.
+    auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
+                    const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
+                    unsigned char* kl_dst, bool vl_do, int vl_key0,
+                    unsigned char* vl_dst) -> float {
+        constexpr int kAhead = 3;
+        constexpr int kMma = 8;  // MFMAs per phase
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        frag p[4];
+        frag fk[kMma];
+        frag fv[kMma];
+        s_next[0] = f32x16{};
+        s_next[1] = f32x16{};
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) fk[k] = k_frag(kt, k);
+#pragma unroll
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fk[i + kAhead] = k_frag(kt, i + kAhead);
+            else fv[i + kAhead - kMma] = v_frag(vt, i + kAhead - kMma);
+            s_next[i >> 2] = Elem<T>::mma(fk[i], qf[i & 3], s_next[i >> 2]);
+            if (i == 1 && kl_do) {
+#pragma unroll
+                for (int part = 0; part < kParts; ++part) load_part(Kh, kl_key0, kl_dst, part);
+            }
+            if (i == 5 && vl_do) {
+#pragma unroll
+                for (int part = 0; part < kParts; ++part) load_part(Vh, vl_key0, vl_dst, part);
+            }
+            exp_one(s, 0, 2 * i, m_use);
+            exp_one(s, 0, 2 * i + 1, m_use);
+            if ((i & 3) == 3) p[i >> 2] = pack_p(s, 0, i >> 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
+        float mx = -INFINITY;
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fv[i + kAhead] = v_frag(vt, i + kAhead);
+            o[i & 1] = Elem<T>::mma(fv[i], p[i >> 1], o[i & 1]);
+            if (i < 4) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) exp_one(s, 1, 4 * i + e, m_use);
+                if (i & 1) p[2 + (i >> 1)] = pack_p(s, 1, i >> 1);
+            }
+            // Row sum of the fp32 exponentials (tile 0 in MFMAs 0-3, tile 1 in MFMAs 4-7).
+            const int t = i >> 2;
+            const int r = 4 * (i & 3);
+            sum += (s[t][r] + s[t][r + 1]) + (s[t][r + 2] + s[t][r + 3]);
+            mx = __builtin_elementwise_maximum(
+                __builtin_elementwise_maximum(mx, s_next[t][r]),
+                __builtin_elementwise_maximum(s_next[t][r + 1],
+                                              __builtin_elementwise_maximum(s_next[t][r + 2],
+                                                                            s_next[t][r + 3])));
+            // Keep both chains here: left alone, the compiler sinks them to their first use.
+            asm volatile("" : "+v"(sum), "+v"(mx));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l += sum;
+        return mx;
+    };
+
+    // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
+    // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
+    // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
+    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and their row max (for the
+    // last block they come from a stale buffer and the max is replaced by -inf, which leaves
+    // (m, l) unchanged). The loop is unrolled by two so that every buffer is a distinct LDS
+    // object.
+    load_tile(Kh, 0, Kb0);
+    load_tile(Vh, 0, Vb0);
+    if (nkb > 1) load_tile(Kh, BN, Kb1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    f32x16 sa[2], sb[2];
+    float alpha;
+    scores(Kb0, sa);
+    if (needs_mask(0)) mask_scores(sa, 0);
+    {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
+        }
+        update_max(mx, alpha);  // O is still zero: nothing to rescale
+    }
+    for (int j = 0; j < nkb; j += 2) {
+        // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                        j + 1 < nkb, (j + 1) * BN, Vb1);
+        if (update_max(j + 1 < nkb ? mx : -INFINITY, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+        if (j + 1 >= nkb) break;
+        // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
+                  j + 2 < nkb, (j + 2) * BN, Vb0);
+        if (update_max(j + 2 < nkb ? mx : -INFINITY, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+    }
+
+    // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
+    l = pair_sum(l);
+    if (q < Nq) {
+        const float inv = 1.0f / l;
+        uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                u32x2 w;
+                w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
+                w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
+                st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // fp32 kernel
 // ------------------------------------------------------------------------------------------
 template <int D>
@@ -687,13 +998,22 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                   hipStream_t stream) {
     using Cfg = dev::Fwd16Cfg<D>;
     constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
-    constexpr int BM = D == 128 ? 32 * kWaves128 : Cfg::BM;
+    constexpr int kWaves64 = 8;   // waves per workgroup of the head_dim 64 kernel
+    constexpr int BM = D == 128 ? 32 * kWaves128 : D == 64 ? 32 * kWaves64 : Cfg::BM;
     const int nqb = (sh.Nq + BM - 1) / BM;
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int coff = sh.Nk - sh.Nq;
     const int tok = profile_kernel<T, D>("forward", stream);
-    if constexpr (D == 128) {
+    if constexpr (D == 64) {
+        hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves64>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0, stream,
+                           reinterpret_cast<const uint16_t*>(Q),
+                           reinterpret_cast<const uint16_t*>(K),
+                           reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
+                           L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
+                           causal ? 1 : 0);
+    } else if constexpr (D == 128) {
         hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
