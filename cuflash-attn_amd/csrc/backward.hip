@@ -459,12 +459,11 @@ __global__ void __launch_bounds__(256, 1)
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
 // without any masking. N is the query length. Block 0 also clears the kNumXcd work-queue
 // counters of the bwd_d128_kernel launch that follows on the stream.
-template <typename T>
+template <typename T, int D>
 __global__ void __launch_bounds__(256)
     delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
                     const float* __restrict__ L, float2* __restrict__ LD, int N, int Npad,
                     long long rows_pad, int* __restrict__ queues) {
-    constexpr int D = 128;
     if (blockIdx.x == 0 && threadIdx.x < kNumXcd) queues[threadIdx.x] = 0;
     constexpr int LPR = D / 8;  // lanes per row
     const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
@@ -494,27 +493,70 @@ __global__ void __launch_bounds__(256)
 // barrier per block; (L log2 e, D) rows come padded from delta_ld_kernel; and the register
 // budget allows two workgroups per CU, so the two waves of each SIMD hide each other's
 // latencies.
-constexpr int kGrp128 = 1088;  // bytes per 4-row group of a 128-wide 16-bit tile
-
-// Per-lane byte offsets into the 4-row-group layout (see fwd16_d128_kernel).
-__device__ __forceinline__ int grp_row_off() {  // A operand: 32 rows x 16 k (row reads)
-    const int lane = threadIdx.x & 63;
-    return ((lane & 31) >> 2) * kGrp128 + (lane >> 5) * 64 + (lane & 3) * 16;
-}
-__device__ __forceinline__ int grp_tr_sub() {  // transpose reads, without the row-half term
-    const int lane = threadIdx.x & 63;
-    const int kq = lane & 15;
-    return (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 + (kq & 1) * 8;
-}
+// LDS layout of a 16-bit tile with D-element rows, as in the forward kernels: rows in groups
+// filled by one 1 KB load instruction each (lane i writes the group's 16-byte slot i).
+//   D = 128 (fwd16_d128_kernel): 4-row groups of 1088 bytes, chunk c of row r at 16 (4 c + r).
+//   D = 64 (fwd16_d64_kernel): 8-row groups of 1152 bytes, chunk c of row r at
+//            16 (8 c + (r ^ 4 ((c >> 1) & 1))).
+// Both serve conflict-free row reads (A operands of 32 rows x 16 k) and transpose reads
+// (A operands whose k runs down 16 rows) with per-lane offsets and immediates.
+template <int D>
+struct TileGroups;
+template <>
+struct TileGroups<128> {
+    static constexpr int kRows = 4;        // rows per group
+    static constexpr int kBytes = 1088;    // bytes per group
+    static constexpr int kKStep = 128;     // row reads: bytes per 16-column k-step
+    static constexpr int kTrRows16 = 4 * kBytes;  // transpose reads: 16 rows further
+    static constexpr int kTrHigh = 2 * kBytes;    // second read of a transpose operand (+8 rows)
+    static constexpr int kTrDTile = 256;          // transpose reads: next 32 columns
+    __device__ static int ld_row(int lane) { return lane & 3; }
+    __device__ static int ld_col(int lane) { return (lane >> 2) * 8; }
+    // Row reads, k-step ks: this lane's 16 bytes (row lane % 32, chunk 2 ks + lane / 32) sit at
+    // row_base(lane, ks & 1) + ks * kKStep.
+    __device__ static int row_base(int lane, int) {
+        return ((lane & 31) >> 2) * kBytes + (lane >> 5) * 64 + (lane & 3) * 16;
+    }
+    // Transpose reads (see tr_frag_at): lane provides the 8-byte chunk of row 4 (lane / 32) +
+    // (lane % 16) / 4, columns 16 ((lane / 16) % 2) + 4 (lane % 4).
+    __device__ static int tr_off(int lane) {
+        const int kq = lane & 15;
+        return (lane >> 5) * kBytes + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 +
+               (kq >> 2) * 16 + (kq & 1) * 8;
+    }
+};
+template <>
+struct TileGroups<64> {
+    static constexpr int kRows = 8;
+    static constexpr int kBytes = 1152;
+    static constexpr int kKStep = 256;
+    static constexpr int kTrRows16 = 2 * kBytes;
+    static constexpr int kTrHigh = kBytes;
+    static constexpr int kTrDTile = 512;
+    __device__ static int ld_row(int lane) { return (lane & 7) ^ (4 * ((lane >> 4) & 1)); }
+    __device__ static int ld_col(int lane) { return (lane >> 3) * 8; }
+    __device__ static int row_base(int lane, int odd) {
+        return ((lane & 31) >> 3) * kBytes + (lane >> 5) * 128 + ((lane & 7) ^ (4 * odd)) * 16;
+    }
+    __device__ static int tr_off(int lane) {
+        const int kq = lane & 15;
+        const int gl = (lane >> 4) & 1;
+        return (2 * gl + ((kq & 3) >> 1)) * 128 + ((lane >> 5) ^ gl) * 64 + (kq >> 2) * 16 +
+               (kq & 1) * 8;
+    }
+};
 
 // Key-stationary part of work item `bid` of heads * nkb (kb = 0, the most work, first); smem
-// holds at least kDkdvLds bytes. Without kShares an item is (key/value head, key block) and runs
+// holds at least dkdv_lds<D>() bytes. Without kShares an item is (key/value head, key block) and runs
 // over all `group` query heads of its key/value head (heads = BHkv), storing dK, dV. With
 // kShares an item is (query head, key block) (heads = BH): it runs over that query head only
 // and stores its fp32 share of dK (scaled) and dV at part[bh] and part[BH + bh] ([BH, Nk, D]
 // each), which dkdv_reduce_kernel sums over each group.
-constexpr int kDkdvLds = 2 * (2 * 8 * kGrp128 + 32 * 8);
-template <typename T, bool kShares>
+template <int D>
+constexpr int dkdv_lds() {  // two sets of Q tile, dO tile and 32 (L, D) rows
+    return 2 * (2 * (32 / TileGroups<D>::kRows) * TileGroups<D>::kBytes + 32 * 8);
+}
+template <typename T, int D, bool kShares>
 __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                                           const uint16_t* __restrict__ K,
                                           const uint16_t* __restrict__ V,
@@ -524,13 +566,15 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
                                           int Nq, int Nk, int coff, int group, int Npad,
                                           int heads, float c, float scale, int causal, int bid,
                                           unsigned char* smem, float* __restrict__ part) {
-    constexpr int D = 128;
+    using G = TileGroups<D>;
     constexpr int BN = 128;  // keys per workgroup (32 per wave)
     constexpr int BM = 32;   // query rows per block
-    constexpr int GRP = kGrp128;
-    constexpr int QT = (BM / 4) * GRP;
+    constexpr int GRP = G::kBytes;
+    constexpr int QT = (BM / G::kRows) * GRP;
     constexpr int SET = 2 * QT + BM * 8;  // Q tile, dO tile, 32 x (L, D)
-    static_assert(2 * SET == kDkdvLds, "LDS size");
+    constexpr int kGroupsPerWave = BM / G::kRows / 4;  // of each 32-row tile
+    constexpr int NDT = D / 32;                        // 32-column tiles of dK, dV
+    static_assert(2 * SET == dkdv_lds<D>(), "LDS size");
     using frag = typename Elem<T>::frag;
 
     int hi, kb;  // item head, key block
@@ -571,8 +615,8 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
     const int span = nqb - qb_begin;
     const int n_it = qheads * span;
 
-    const int ld_row = lane & 3;
-    const int ld_col = (lane >> 2) * 8;
+    const int ld_row = G::ld_row(lane);
+    const int ld_col = G::ld_col(lane);
     auto load_block = [&](int it, int b) {
         const int bh = bq0 + it / span;
         const int r0 = (qb_begin + it % span) * BM;
@@ -582,16 +626,16 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
         unsigned char* set = smem + b * SET;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kGroupsPerWave; ++i) {
             const int grp = wave + 4 * i;
-            const int row = min(r0 + 4 * grp + ld_row, Nq - 1);
+            const int row = min(r0 + G::kRows * grp + ld_row, Nq - 1);
             lds_dma16_async(Qh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
             lds_dma16_async(Oh + static_cast<size_t>(row) * D + ld_col, set + QT + grp * GRP);
         }
         if (wave == 3) lds_dma4_async(LDh + 2 * r0 + lane, set + 2 * QT);
     };
-    const int row_off = grp_row_off();
-    const int tr_off = g2 * GRP + grp_tr_sub();
+    const int row_base[2] = {G::row_base(lane, 0), G::row_base(lane, 1)};
+    const int tr_off = G::tr_off(lane);
 
     f32x16 dk[D / 32];
     f32x16 dv[D / 32];
@@ -619,18 +663,19 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         f32x16 dp = f32x16{};
         {
             constexpr int kAhead = 3;
-            frag fa[16];
+            constexpr int kMma = 2 * (D / 16);
+            frag fa[kMma];
+            auto operand = [&](int k) {
+                const int ks = k >> 1;
+                return as_frag<T>(ld16((k & 1 ? ot : qt) + row_base[ks & 1] + ks * G::kKStep));
+            };
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < kMma; ++i) {
                 if (i == 0) {
 #pragma unroll
-                    for (int k = 0; k < kAhead; ++k)
-                        fa[k] = as_frag<T>(ld16((k & 1 ? ot : qt) + row_off + (k >> 1) * 128));
+                    for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
                 }
-                if (i + kAhead < 16) {
-                    const int k = i + kAhead;
-                    fa[k] = as_frag<T>(ld16((k & 1 ? ot : qt) + row_off + (k >> 1) * 128));
-                }
+                if (i + kAhead < kMma) fa[i + kAhead] = operand(i + kAhead);
                 if (i & 1)
                     dp = Elem<T>::mma(fa[i], vf[i >> 1], dp);
                 else
@@ -675,21 +720,23 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
         // (j = i / 8, dt = (i / 2) % 4; even: dO^T, odd: Q^T) is read kAhead MFMAs ahead.
         {
             constexpr int kAhead = 3;
-            frag fa[16];
+            constexpr int kMma = 4 * NDT;  // (dV, dK) x 2 query halves x NDT column tiles
+            frag fa[kMma];
             auto operand = [&](int i) {
-                const unsigned char* a =
-                    (i & 1 ? qt : ot) + tr_off + (i >> 3) * 4 * GRP + ((i >> 1) & 3) * 256;
-                return tr_frag_at<T>(a, a + 2 * GRP);
+                const unsigned char* a = (i & 1 ? qt : ot) + tr_off +
+                                         (i / (2 * NDT)) * G::kTrRows16 +
+                                         ((i >> 1) % NDT) * G::kTrDTile;
+                return tr_frag_at<T>(a, a + G::kTrHigh);
             };
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < kMma; ++i) {
                 if (i == 0) {
 #pragma unroll
                     for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
                 }
-                if (i + kAhead < 16) fa[i + kAhead] = operand(i + kAhead);
-                const int j = i >> 3;
-                const int dt = (i >> 1) & 3;
+                if (i + kAhead < kMma) fa[i + kAhead] = operand(i + kAhead);
+                const int j = i / (2 * NDT);
+                const int dt = (i >> 1) % NDT;
                 if (i & 1)
                     dk[dt] = Elem<T>::mma(fa[i], bs[j], dk[dt]);
                 else
@@ -738,9 +785,12 @@ __device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
 }
 
 // Query-stationary part of workgroup `bid` of BH * nqb (causal: the longest query blocks
-// first); smem holds at least kDqLds bytes.
-constexpr int kDqLds = 2 * 2 * 8 * kGrp128;
-template <typename T>
+// first); smem holds at least dq_lds<D>() bytes.
+template <int D>
+constexpr int dq_lds() {  // two sets of K tile and V tile
+    return 2 * 2 * (32 / TileGroups<D>::kRows) * TileGroups<D>::kBytes;
+}
+template <typename T, int D>
 __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
                                         const uint16_t* __restrict__ K,
                                         const uint16_t* __restrict__ V,
@@ -749,13 +799,15 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
                                         uint16_t* __restrict__ dQ, int Nq, int Nk, int coff,
                                         int group, int Npad, int nqb, int BH, float c,
                                         float scale, int causal, int bid, unsigned char* smem) {
-    constexpr int D = 128;
+    using G = TileGroups<D>;
     constexpr int BM = 128;  // query rows per workgroup (32 per wave)
     constexpr int BN = 32;   // keys per block
-    constexpr int GRP = kGrp128;
-    constexpr int KT = (BN / 4) * GRP;
+    constexpr int GRP = G::kBytes;
+    constexpr int KT = (BN / G::kRows) * GRP;
     constexpr int SET = 2 * KT;  // K tile, V tile
-    static_assert(2 * SET == kDqLds, "LDS size");
+    constexpr int kGroupsPerWave = BN / G::kRows / 4;
+    constexpr int NDT = D / 32;  // 32-column tiles of dQ
+    static_assert(2 * SET == dq_lds<D>(), "LDS size");
     using frag = typename Elem<T>::frag;
 
     int bh, rank;
@@ -790,21 +842,21 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
     // (L log2 e, D) of this lane's query; padding rows give P = 0.
     const float2 ldq = (q < Npad) ? LD[static_cast<size_t>(bh) * Npad + q] : make_float2(INFINITY, 0.0f);
 
-    const int ld_row = lane & 3;
-    const int ld_col = (lane >> 2) * 8;
+    const int ld_row = G::ld_row(lane);
+    const int ld_col = G::ld_col(lane);
     auto load_block = [&](int kb, int b) {
         const int r0 = kb * BN;
         unsigned char* set = smem + b * SET;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kGroupsPerWave; ++i) {
             const int grp = wave + 4 * i;
-            const int row = min(r0 + 4 * grp + ld_row, Nk - 1);
+            const int row = min(r0 + G::kRows * grp + ld_row, Nk - 1);
             lds_dma16_async(Kh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
             lds_dma16_async(Vh + static_cast<size_t>(row) * D + ld_col, set + KT + grp * GRP);
         }
     };
-    const int row_off = grp_row_off();
-    const int tr_off = g2 * GRP + grp_tr_sub();
+    const int row_base[2] = {G::row_base(lane, 0), G::row_base(lane, 1)};
+    const int tr_off = G::tr_off(lane);
 
     f32x16 acc[D / 32];
 #pragma unroll
@@ -829,18 +881,19 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
         f32x16 dp = f32x16{};
         {
             constexpr int kAhead = 3;
-            frag fa[16];
+            constexpr int kMma = 2 * (D / 16);
+            frag fa[kMma];
+            auto operand = [&](int k) {
+                const int ks = k >> 1;
+                return as_frag<T>(ld16((k & 1 ? vt : kt) + row_base[ks & 1] + ks * G::kKStep));
+            };
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < kMma; ++i) {
                 if (i == 0) {
 #pragma unroll
-                    for (int k = 0; k < kAhead; ++k)
-                        fa[k] = as_frag<T>(ld16((k & 1 ? vt : kt) + row_off + (k >> 1) * 128));
+                    for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
                 }
-                if (i + kAhead < 16) {
-                    const int k = i + kAhead;
-                    fa[k] = as_frag<T>(ld16((k & 1 ? vt : kt) + row_off + (k >> 1) * 128));
-                }
+                if (i + kAhead < kMma) fa[i + kAhead] = operand(i + kAhead);
                 if (i & 1)
                     dp = Elem<T>::mma(fa[i], of[i >> 1], dp);
                 else
@@ -868,19 +921,21 @@ __device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
                 bsf[j] = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
                                       s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
             constexpr int kAhead = 3;
-            frag fa[8];
+            constexpr int kMma = 2 * NDT;  // 2 key halves x NDT column tiles
+            frag fa[kMma];
             auto operand = [&](int i) {
-                const unsigned char* a = kt + tr_off + (i >> 2) * 4 * GRP + (i & 3) * 256;
-                return tr_frag_at<T>(a, a + 2 * GRP);
+                const unsigned char* a =
+                    kt + tr_off + (i / NDT) * G::kTrRows16 + (i % NDT) * G::kTrDTile;
+                return tr_frag_at<T>(a, a + G::kTrHigh);
             };
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < kMma; ++i) {
                 if (i == 0) {
 #pragma unroll
                     for (int k = 0; k < kAhead; ++k) fa[k] = operand(k);
                 }
-                if (i + kAhead < 8) fa[i + kAhead] = operand(i + kAhead);
-                acc[i & 3] = Elem<T>::mma(fa[i], bsf[i >> 2], acc[i & 3]);
+                if (i + kAhead < kMma) fa[i + kAhead] = operand(i + kAhead);
+                acc[i % NDT] = Elem<T>::mma(fa[i], bsf[i / NDT], acc[i % NDT]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -916,7 +971,7 @@ __device__ __forceinline__ int xcc_id() {
            (kNumXcd - 1);  // HW_REG_XCC_ID[3:0]
 }
 
-template <typename T, bool kShares>
+template <typename T, int D, bool kShares>
 __global__ void __launch_bounds__(256, 2)
     bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
@@ -924,7 +979,7 @@ __global__ void __launch_bounds__(256, 2)
                     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int Nq, int Nk,
                     int coff, int group, int Npad, int nqb, int nkb, int BH, float c,
                     float scale, int causal, int* __restrict__ queues, float* __restrict__ part) {
-    constexpr int kLds = kDkdvLds > kDqLds ? kDkdvLds : kDqLds;
+    constexpr int kLds = dkdv_lds<D>() > dq_lds<D>() ? dkdv_lds<D>() : dq_lds<D>();
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
     __shared__ int item;
     const int dkdv_heads = kShares ? BH : BH / group;  // see dkdv_d128
@@ -953,11 +1008,11 @@ __global__ void __launch_bounds__(256, 2)
         if (it < 0) break;
         const int id = it & ((1 << 30) - 1);
         if (it >> 30)
-            dq_d128<T>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
-                       causal, id, smem);
+            dq_d128<T, D>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
+                          causal, id, smem);
         else
-            dkdv_d128<T, kShares>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad,
-                                  dkdv_heads, c, scale, causal, id, smem, part);
+            dkdv_d128<T, D, kShares>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad,
+                                     dkdv_heads, c, scale, causal, id, smem, part);
         __syncthreads();  // the next item reuses the LDS tiles
     }
 }
@@ -1070,13 +1125,13 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     return err;
 }
 
-// Path for head_dim 128: delta_ld_kernel, then bwd_d128_kernel (dq and dkdv in one launch).
-template <typename T>
+// Path for fp16 / bf16 at head_dim 128 and 64: delta_ld_kernel, then bwd_d128_kernel (dq and
+// dkdv in one launch).
+template <typename T, int D>
 FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* V, const T* O,
                                                const float* L, const T* dO, T* dQ, T* dK, T* dV,
                                                const BwdShape& sh, float scale, bool causal,
                                                hipStream_t stream) {
-    constexpr int D = 128;
     const int Npad = (sh.Nq + 31) / 32 * 32;
     const long long rows_pad = static_cast<long long>(sh.BH) * Npad;
     StreamWorkspace ws(stream);
@@ -1107,7 +1162,7 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     const uint16_t* go = reinterpret_cast<const uint16_t*>(dO);
 
     int tok = profile_kernel<T, D>("backward_delta", stream);
-    hipLaunchKernelGGL((dev::delta_ld_kernel<T>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
+    hipLaunchKernelGGL((dev::delta_ld_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, sh.Nq, Npad,
                        rows_pad, queues);
     profile_end(tok, stream);
@@ -1125,7 +1180,7 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     // Two resident workgroups per CU take the qblocks + kblocks work items.
     const long long pool = std::min<long long>(qblocks + kblocks, 2LL * compute_units());
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
-    auto kernel = shares ? dev::bwd_d128_kernel<T, true> : dev::bwd_d128_kernel<T, false>;
+    auto kernel = shares ? dev::bwd_d128_kernel<T, D, true> : dev::bwd_d128_kernel<T, D, false>;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
                        ld, go, reinterpret_cast<uint16_t*>(dQ), reinterpret_cast<uint16_t*>(dK),
                        reinterpret_cast<uint16_t*>(dV), sh.Nq, sh.Nk, sh.Nk - sh.Nq, sh.group,
@@ -1150,9 +1205,9 @@ FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* 
                                    const float* L, const T* dO, T* dQ, T* dK, T* dV,
                                    const BwdShape& sh, float scale, bool causal,
                                    hipStream_t stream) {
-    if constexpr (!std::is_same<T, float>::value && D == 128)
-        return run_backward_two_pass_d128<T>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
-                                             stream);
+    if constexpr (!std::is_same<T, float>::value && (D == 128 || D == 64))
+        return run_backward_two_pass_d128<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+                                                stream);
     else
         return run_backward_two_pass<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                            stream);
