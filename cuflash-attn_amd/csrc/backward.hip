@@ -18,8 +18,8 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
-// For fp16/bf16 at head_dim 128 the same steps run as delta_ld_kernel, then dq_d128 and
-// dkdv_d128 side by side in one launch (bwd_d128_kernel, section 4). Every path is
+// For fp16/bf16 at head_dim 128 and 64 the same steps run as delta_ld_kernel, then dq_lds_tiles
+// and dkdv_lds_tiles items in one launch (bwd_fused_kernel, section 4). Every path is
 // deterministic: no atomics, and each output element is written by exactly one lane.
 //
 // Shapes: Q, O, dO, dQ are [BH, Nq, D], K, V, dK, dV are [BH / group, Nk, D] (query head bh
@@ -453,12 +453,12 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// 4. Backward for head_dim 128 (fp16 / bf16)
+// 4. Backward for head_dim 128 and 64 (fp16 / bf16)
 // ------------------------------------------------------------------------------------------
-// Row statistics for the D = 128 kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
+// Row statistics for bwd_fused_kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
 // without any masking. N is the query length. Block 0 also clears the kNumXcd work-queue
-// counters of the bwd_d128_kernel launch that follows on the stream.
+// counters of the bwd_fused_kernel launch that follows on the stream.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
@@ -484,11 +484,12 @@ __global__ void __launch_bounds__(256)
 }
 
 // ------------------------------------------------------------------------------------------
-// dkdv_d128 and dq_d128 restate dkdv_kernel and dq_kernel (same products, same
+// dkdv_lds_tiles and dq_lds_tiles restate dkdv_kernel and dq_kernel (same products, same
 // rounding of P and dS to T) with a gfx950 data path: tiles go global -> LDS by direct loads
 // (global_load_lds_dwordx4, issued from inline assembly so that buffers can rotate at run time)
-// into the padded 4-row-group layout of fwd16_d128_kernel, whose single copy of a tile serves
-// both the row reads of S = Q K^T / dP = dO V^T and the transpose reads of dV^T += dO^T P /
+// into the padded row-group layout of the forward kernels (TileGroups below), whose single copy
+// of a tile serves both the row reads of S = Q K^T / dP = dO V^T and the transpose reads of
+// dV^T += dO^T P /
 // dK^T += Q^T dS / dQ^T += K^T dS^T without bank conflicts; blocks are double-buffered with one
 // barrier per block; (L log2 e, D) rows come padded from delta_ld_kernel; and the register
 // budget allows two workgroups per CU, so the two waves of each SIMD hide each other's
@@ -557,7 +558,7 @@ constexpr int dkdv_lds() {  // two sets of Q tile, dO tile and 32 (L, D) rows
     return 2 * (2 * (32 / TileGroups<D>::kRows) * TileGroups<D>::kBytes + 32 * 8);
 }
 template <typename T, int D, bool kShares>
-__device__ __forceinline__ void dkdv_d128(const uint16_t* __restrict__ Q,
+__device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
                                           const uint16_t* __restrict__ K,
                                           const uint16_t* __restrict__ V,
                                           const float2* __restrict__ LD,
@@ -791,7 +792,7 @@ constexpr int dq_lds() {  // two sets of K tile and V tile
     return 2 * 2 * (32 / TileGroups<D>::kRows) * TileGroups<D>::kBytes;
 }
 template <typename T, int D>
-__device__ __forceinline__ void dq_d128(const uint16_t* __restrict__ Q,
+__device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
                                         const uint16_t* __restrict__ K,
                                         const uint16_t* __restrict__ V,
                                         const float2* __restrict__ LD,
@@ -973,7 +974,7 @@ __device__ __forceinline__ int xcc_id() {
 
 template <typename T, int D, bool kShares>
 __global__ void __launch_bounds__(256, 2)
-    bwd_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    bwd_fused_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
                     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int Nq, int Nk,
@@ -982,7 +983,7 @@ __global__ void __launch_bounds__(256, 2)
     constexpr int kLds = dkdv_lds<D>() > dq_lds<D>() ? dkdv_lds<D>() : dq_lds<D>();
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kLds];
     __shared__ int item;
-    const int dkdv_heads = kShares ? BH : BH / group;  // see dkdv_d128
+    const int dkdv_heads = kShares ? BH : BH / group;  // see dkdv_lds_tiles
     const int n_dq = BH * nqb;
     const int n_dkdv = dkdv_heads * nkb;
     const int home = xcc_id();
@@ -1008,17 +1009,17 @@ __global__ void __launch_bounds__(256, 2)
         if (it < 0) break;
         const int id = it & ((1 << 30) - 1);
         if (it >> 30)
-            dq_d128<T, D>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
+            dq_lds_tiles<T, D>(Q, K, V, LD, dO, dQ, Nq, Nk, coff, group, Npad, nqb, BH, c, scale,
                           causal, id, smem);
         else
-            dkdv_d128<T, D, kShares>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad,
+            dkdv_lds_tiles<T, D, kShares>(Q, K, V, LD, dO, dK, dV, Nq, Nk, coff, group, Npad,
                                      dkdv_heads, c, scale, causal, id, smem, part);
         __syncthreads();  // the next item reuses the LDS tiles
     }
 }
 
 // dK, dV of each key/value head from the fp32 shares of its `group` query heads (the
-// part != nullptr mode of dkdv_d128): part holds dK shares [BH, Nk, D], then dV shares. Eight
+// part != nullptr mode of dkdv_lds_tiles): part holds dK shares [BH, Nk, D], then dV shares. Eight
 // elements per thread; sums in fp32 in head order, one rounding to T.
 template <typename T>
 __global__ void __launch_bounds__(256)
@@ -1125,17 +1126,17 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     return err;
 }
 
-// Path for fp16 / bf16 at head_dim 128 and 64: delta_ld_kernel, then bwd_d128_kernel (dq and
+// Path for fp16 / bf16 at head_dim 128 and 64: delta_ld_kernel, then bwd_fused_kernel (dq and
 // dkdv in one launch).
 template <typename T, int D>
-FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* V, const T* O,
+FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const T* O,
                                                const float* L, const T* dO, T* dQ, T* dK, T* dV,
                                                const BwdShape& sh, float scale, bool causal,
                                                hipStream_t stream) {
     const int Npad = (sh.Nq + 31) / 32 * 32;
     const long long rows_pad = static_cast<long long>(sh.BH) * Npad;
     StreamWorkspace ws(stream);
-    // (L log2 e, D) rows, then the kNumXcd work-queue counters of bwd_d128_kernel
+    // (L log2 e, D) rows, then the kNumXcd work-queue counters of bwd_fused_kernel
     const size_t ld_bytes = static_cast<size_t>(rows_pad) * sizeof(float2);
     FlashAttentionError err = ws.alloc(ld_bytes + dev::kNumXcd * sizeof(int));
     if (err != FlashAttentionError::SUCCESS) return err;
@@ -1180,7 +1181,7 @@ FlashAttentionError run_backward_two_pass_d128(const T* Q, const T* K, const T* 
     // Two resident workgroups per CU take the qblocks + kblocks work items.
     const long long pool = std::min<long long>(qblocks + kblocks, 2LL * compute_units());
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
-    auto kernel = shares ? dev::bwd_d128_kernel<T, D, true> : dev::bwd_d128_kernel<T, D, false>;
+    auto kernel = shares ? dev::bwd_fused_kernel<T, D, true> : dev::bwd_fused_kernel<T, D, false>;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
                        ld, go, reinterpret_cast<uint16_t*>(dQ), reinterpret_cast<uint16_t*>(dK),
                        reinterpret_cast<uint16_t*>(dV), sh.Nq, sh.Nk, sh.Nk - sh.Nq, sh.group,
@@ -1206,7 +1207,7 @@ FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* 
                                    const BwdShape& sh, float scale, bool causal,
                                    hipStream_t stream) {
     if constexpr (!std::is_same<T, float>::value && (D == 128 || D == 64))
-        return run_backward_two_pass_d128<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
+        return run_backward_fused<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                                 stream);
     else
         return run_backward_two_pass<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
