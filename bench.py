@@ -213,8 +213,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (every "
-              "kernel here runs on a single MI355X; see DESIGN.md for how the path would shard)",
-              file=sys.stderr)
+              "kernel here runs on a single MI355X; sharding over heads or keys across GPUs "
+              "is not built)", file=sys.stderr)
         return 2
 
     if args.pmc_workload:
