@@ -369,6 +369,27 @@ def main():
         ld = torch.empty((Bd, Hd, 1), device=dev, dtype=torch.float32)
         dec = lib.fn("decode", "f16")
         nbytes = decode_bytes(Bd, Hd, LKV, Dd)
+
+        def time_calls(fn):
+            """ms per call over args.steps calls with no event hook (the hook's events between
+            the split and combine launches cost time of their own), then the per-kernel
+            report of a second pass with the hook on."""
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            t0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / args.steps
+            lib.profile_enable(True)
+            for _ in range(args.steps):
+                fn()
+            torch.cuda.synchronize()
+            rep = lib.profile_report()
+            lib.profile_enable(False)
+            return ms, rep
         results = {}
         for splits in (16, 32, 64, 0):
             def run():
@@ -376,18 +397,7 @@ def main():
                          ld.data_ptr(), Bd, Hd, LKV, Dd, Dd ** -0.5, splits, sp)
                 if st != 0:
                     raise RuntimeError(f"decode status {st}")
-            for _ in range(3):
-                run()
-            torch.cuda.synchronize()
-            lib.profile_enable(True)
-            t0.record(stream)
-            for _ in range(args.steps):
-                run()
-            t1.record(stream)
-            torch.cuda.synchronize()
-            rep = lib.profile_report()
-            lib.profile_enable(False)
-            ms = t0.elapsed_time(t1) / args.steps
+            ms, rep = time_calls(run)
             split_ms = rep.get(f"decode_split_f16_d{Dd}", (1, float("nan")))
             results["auto" if splits == 0 else str(splits)] = {
                 "ms": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -415,18 +425,7 @@ def main():
         ext_bytes = Bd * Hkv * LKV * Dd * 2 * 2 + Bd * Hd * Dd * 2 * 2 + Bd * Hd * 4
 
         def time_ext(fn, label):
-            for _ in range(3):
-                fn()
-            torch.cuda.synchronize()
-            lib.profile_enable(True)
-            t0.record(stream)
-            for _ in range(args.steps):
-                fn()
-            t1.record(stream)
-            torch.cuda.synchronize()
-            rep = lib.profile_report()
-            lib.profile_enable(False)
-            ms = t0.elapsed_time(t1) / args.steps
+            ms, rep = time_calls(fn)
             sk = rep.get(f"decode_split_f16_d{Dd}", (1, float("nan")))
             return {"ms": round(ms, 4), "GB/s": round(ext_bytes / (ms * 1e-3) / 1e9, 1),
                     "split_kernel_ms": round(sk[1] / sk[0], 4),
