@@ -123,3 +123,34 @@ def test_prefill_chunk_equals_rows_of_full_causal_attention(torch_gpu, dtype):
     torch_gpu.cuda.synchronize()
     assert float((o.float() - o_full[:, :, n - nq:].float()).abs().max()) <= 1e-2
     assert float((lse - l_full[:, :, n - nq:]).abs().max()) <= 1e-4
+
+
+@pytest.mark.gpu
+def test_gqa_backward_without_shares_matches_expanded_heads(torch_gpu):
+    """Grouped heads whose fp32 dK/dV shares would exceed 2 GiB (64 query heads x 32768 keys)
+    take the per-key/value-head dkdv items that sum the group in registers. Checked against the
+    same library on K/V repeated per query head (no grouping): dQ is computed identically
+    (bitwise equal), dK and dV are the sums over each group (fp32 here, one rounding there)."""
+    import torch
+
+    B, H, Hkv, nq, nk, d = 1, 64, 8, 128, 32768, 128
+    group = H // Hkv
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    q, do = (torch.rand((B, H, nq, d), generator=g, device="cuda") * 2 - 1 for _ in range(2))
+    k, v = (torch.rand((B, Hkv, nk, d), generator=g, device="cuda") * 2 - 1 for _ in range(2))
+    q, do, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, do, k, v))
+    o, lse = cuflash_attn.flash_attention_forward_ext(q, k, v, causal=True)
+    dq, dk, dv = cuflash_attn.flash_attention_backward_ext(q, k, v, o, lse, do, causal=True)
+    ke = torch.repeat_interleave(k, group, dim=1).contiguous()
+    ve = torch.repeat_interleave(v, group, dim=1).contiguous()
+    o2, lse2 = cuflash_attn.flash_attention_forward_ext(q, ke, ve, causal=True)
+    dq2, dk2, dv2 = cuflash_attn.flash_attention_backward_ext(q, ke, ve, o2, lse2, do,
+                                                              causal=True)
+    torch_gpu.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(dq, dq2)
+    dk_sum = dk2.float().reshape(B, Hkv, group, nk, d).sum(2)
+    dv_sum = dv2.float().reshape(B, Hkv, group, nk, d).sum(2)
+    assert float((dk.float() - dk_sum).abs().max()) <= 2e-2
+    assert float((dv.float() - dv_sum).abs().max()) <= 2e-2
