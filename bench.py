@@ -488,6 +488,17 @@ def main():
                          f"fwd+bwd, naive O(N^2) fp32 (reference test_forward.cu:21-118 / "
                          f"test_backward.cu:21-127 restated in C), one thread per head, same "
                          f"FLOP model"}
+        # One thread on one head of half the length (a quarter of a head's work at N = ncpu).
+        n1 = max(64, ncpu // 2)
+        x1 = [x[:, :1, :n1] for x in xs]
+        c0 = time.perf_counter()
+        oracle.naive_forward_f32(x1[0], x1[1], x1[2], scale, causal, nthreads=1)
+        oracle.naive_backward_f32(x1[0], x1[1], x1[2], x1[3], scale, causal, nthreads=1)
+        secs1 = time.perf_counter() - c0
+        cpu["single_thread"] = {
+            "value": round(flops_fwd(1, 1, n1, D, causal) * 3.5 / secs1 / 1e12, 6),
+            "unit": "TFLOP/s", "cores": 1, "seconds": round(secs1, 2),
+            "sample": f"the same loops on one head of N={n1}, one thread"}
 
     out = {
         "metric": "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM GB/s at 32k KV",
