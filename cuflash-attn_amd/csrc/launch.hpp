@@ -74,10 +74,11 @@ inline FlashAttentionError from_hip(hipError_t e) {
 // Compute units of the current device (cached per device; 256 on MI355X when the query fails).
 int compute_units();
 
-// The library's own stream-ordered memory pool on the current device (created on first use,
-// kept until the process ends, release threshold at its maximum so that freed blocks stay in the
-// pool and later allocations of the same size need no driver call). Using a private pool leaves
-// the application's default pool and its settings untouched. nullptr when it cannot be created.
+// The library's own stream-ordered memory pool on the current device (created on first use and
+// kept until the process ends; up to 256 MiB of freed blocks stay in the pool across
+// synchronizations, so later allocations of the same size need no driver call). Using a private
+// pool leaves the application's default pool and its settings untouched. nullptr when it cannot
+// be created (the workspaces then come from the device's current pool).
 hipMemPool_t workspace_pool();
 
 // Stream-ordered device workspace (hipMallocFromPoolAsync / hipFreeAsync on the caller's stream),

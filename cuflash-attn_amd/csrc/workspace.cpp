@@ -2,8 +2,9 @@
 //
 // hipMallocAsync from a pool whose release threshold is 0 (the default) hands freed memory back
 // at every synchronization, so each call's workspace needs fresh driver work. A private pool per
-// device with the threshold at its maximum keeps the few MiB the launchers use (the backward's
-// row statistics, the decode partials) cached, and leaves the application's pools alone.
+// device whose release threshold is kKeepBytes keeps the few MiB the launchers usually use (the
+// backward's row statistics, the decode partials) cached, gives larger workspaces (grouped-query
+// dK/dV shares) back at synchronization, and leaves the application's pools alone.
 
 #include <cstdint>
 #include <mutex>
@@ -15,6 +16,7 @@ namespace detail {
 
 namespace {
 constexpr int kMaxDevices = 64;
+constexpr uint64_t kKeepBytes = 256ull << 20;  // pool memory kept across synchronizations
 std::mutex g_pool_mutex;
 hipMemPool_t g_pools[kMaxDevices] = {};
 bool g_tried[kMaxDevices] = {};
@@ -36,14 +38,16 @@ hipMemPool_t workspace_pool() {
         props.location.id = dev;
         hipMemPool_t pool = nullptr;
         if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
-            uint64_t keep = UINT64_MAX;
+            uint64_t keep = kKeepBytes;
             if (hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) == hipSuccess) {
                 g_pools[dev] = pool;
             } else {
+                (void)hipGetLastError();  // clear only the error of this call
                 (void)hipMemPoolDestroy(pool);
             }
+        } else {
+            (void)hipGetLastError();
         }
-        (void)hipGetLastError();
     }
     return g_pools[dev];
 }
