@@ -519,6 +519,303 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 }
 
 // ------------------------------------------------------------------------------------------
+// fp16 / bf16 kernel for head_dim 256
+// ------------------------------------------------------------------------------------------
+// fwd16_d128_kernel's data path and pipeline at head_dim 256: a 4-row group holds the two
+// 128-column halves of its rows one after the other, each in the 1 KB layout of the head_dim-128
+// groups, plus 64 bytes of padding (so row reads and transpose reads stay conflict-free as
+// there). O (8 accumulator tiles) and Q^T (16 fragments) need one workgroup of NW waves per
+// CU, i.e. one wave per SIMD for NW = 4.
+template <typename T, int NW>
+__global__ void __launch_bounds__(64 * NW, 1)
+    fwd16_d256_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                      const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
+                      float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
+                      float c, int causal) {
+    constexpr int D = 256;
+    constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
+    constexpr int BN = 64;
+    constexpr int kParts = 32 / NW;  // load instructions per wave per 64-row tile
+    constexpr int HALF = 1024;             // bytes of one 128-column half of a 4-row group
+    constexpr int GRP = 2 * HALF + 64;     // bytes per 4-row group
+    constexpr int TILE = (BN / 4) * GRP;   // bytes per 64-row tile
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
+
+    int bh, rank;
+    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
+    const int q0 = qb * BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;              // query row owned by this lane
+
+    frag qf[D / 16];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < Nq) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    const int kv_end = causal ? min(Nk, (qb + 1) * BM + coff) : Nk;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    // Loads of one 64-row tile: 16 groups of 4 rows, two load instructions per group (columns
+    // 0-127 and 128-255, 1 KB each, in the layout of fwd16_d128_kernel's groups). Part i of a
+    // wave loads half i % 2 of group wave + NW (i / 2). Rows past Nk are clamped to row Nk - 1.
+    const int ld_row = lane & 3;
+    const int ld_col = (lane >> 2) * 8;
+    const unsigned ld_voff = static_cast<unsigned>(((4 * wave + ld_row) * D + ld_col) * 2);
+    auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
+        const int grp = wave + NW * (i >> 1);
+        const int half = i & 1;
+        if (key0 + BN <= Nk) {
+            lds_dma16_async_s(src + static_cast<size_t>(key0 + 4 * NW * (i >> 1)) * D + 128 * half,
+                              ld_voff, dst + grp * GRP + half * HALF);
+        } else {
+            const int row = min(key0 + 4 * grp + ld_row, Nk - 1);
+            lds_dma16_async(src + static_cast<size_t>(row) * D + 128 * half + ld_col,
+                            dst + grp * GRP + half * HALF);
+        }
+    };
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+#pragma unroll
+        for (int i = 0; i < kParts; ++i) load_part(src, key0, dst, i);
+    };
+    // Per-lane byte offsets of the operand reads (see the layout above).
+    const int k_off = (l32 >> 2) * GRP + g2 * 64 + (l32 & 3) * 16;
+    const int kq = lane & 15;
+    const int v_off = g2 * GRP + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 +
+                      (kq & 1) * 8;
+
+    // K row reads, k-step ks (16 columns): half ks / 8, chunk 2 (ks % 8) + lane / 32.
+    auto k_addr = [&](const unsigned char* kt, int t, int ks) {
+        return kt + k_off + 8 * t * GRP + (ks >> 3) * HALF + (ks & 7) * 128;
+    };
+    auto scores = [&](const unsigned char* kt, f32x16 (&s)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks)
+                s[t] = Elem<T>::mma(as_frag<T>(ld16(k_addr(kt, t, ks))), qf[ks], s[t]);
+        }
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;  // running max of s * cs (log2 units)
+    float l = 0.0f;       // this lane's share of the running row sum
+    // Exponent scale, kept positive so that a masked score (-inf) always maps to p = 0, also
+    // for scale = 0 (where FLT_MIN leaves every p at 1 and L at log(count), as with 0).
+    const float cs = fmaxf(c, kFltMin);
+
+    // Keys past Nk and, with a causal mask, keys after this lane's row get s = -inf.
+    auto mask_scores = [&](f32x16 (&s)[2], int key0) {
+        const int lim = min(Nk, causal ? q + 1 + coff : Nk) - key0 - 4 * g2;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int off = 32 * t + 8 * (r >> 2) + (r & 3);
+                s[t][r] = off < lim ? s[t][r] : -INFINITY;
+            }
+        }
+    };
+
+    // Online-softmax update of (m, l) from mx, this lane's raw row max of the next block.
+    // Returns whether some lane of the wave must rescale its O by alpha. The lazy rescale is
+    // decided per lane with selects: m only moves when the block max exceeds it by more than
+    // kLazyRescale, and O and l of that lane are scaled by the same alpha, so the result is
+    // exact either way.
+    auto update_max = [&](float mx, float& alpha) -> bool {
+        const float m_new = fmaxf(m, pair_max(mx) * cs);
+        const bool grow = m_new > m + kLazyRescale;
+        const float a_raw = fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new);
+        alpha = grow ? a_raw : 1.0f;
+        m = grow ? m_new : m;
+        l *= alpha;
+        return __ballot(grow) != 0;
+    };
+
+    // Operand fragment i of the score MFMAs (K rows of tile i / 16, k-step i % 16) and of
+    // the P V MFMAs (V^T for key group i / 8 and d tile i % 8: half (i % 8) / 4).
+    auto k_frag = [&](const unsigned char* kt, int i) {
+        return as_frag<T>(ld16(k_addr(kt, i >> 4, i & 15)));
+    };
+    auto v_frag = [&](const unsigned char* vt, int i) {
+        const int dt = i & 7;
+        const unsigned char* a0 =
+            vt + v_off + 4 * (i >> 3) * GRP + (dt >> 2) * HALF + (dt & 3) * 256;
+        return tr_frag_at<T>(a0, a0 + 2 * GRP);
+    };
+
+    // Blocks that need masking: keys past Nk, and with a causal mask the blocks that reach past
+    // the last key this wave's first row sees.
+    auto needs_mask = [&](int key0) {
+        return key0 + BN > Nk || (causal && key0 + BN - 1 > q0 + coff);
+    };
+
+    // Exponential of score r of tile t, and the rounding of tile t's group h of eight scores
+    // to T (the P operand of key group 2 t + h).
+    auto exp_one = [&](f32x16 (&s)[2], int t, int r, float m_use) {
+        s[t][r] = fast_exp2(fmaf(s[t][r], cs, -m_use));
+    };
+    auto pack_p = [&](f32x16 (&s)[2], int t, int h) {
+        u32x4 pw = __builtin_bit_cast(
+            u32x4, pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2],
+                                s[t][8 * h + 3], s[t][8 * h + 4], s[t][8 * h + 5],
+                                s[t][8 * h + 6], s[t][8 * h + 7]));
+        // Keep the exponentials where they are placed: left alone, the compiler sinks them
+        // to their first use past the branches in between.
+        asm volatile("" : "+v"(pw));
+        return __builtin_bit_cast(frag, pw);
+    };
+
+    // One block with an explicit instruction order (the scheduling fences keep it), as in
+    // fwd16_d128_kernel with twice the MFMAs per phase:
+    //   phase A: the 32 MFMAs of the next block's scores into s_next; every other one followed
+    //            by the exponential of one score of the current tile 0 (P groups 0 and 1); the
+    //            wave's 2 kParts tile-load parts after every other odd MFMA (K in the first half,
+    //            V in the second);
+    //   phase B: the 32 MFMAs of O^T += V^T P^T; MFMAs 0-15 carry the exponentials of tile 1
+    //            (P groups 2 and 3, first used by MFMAs 16 and 24), every MFMA one term of the
+    //            fp32 row sum and the max of one score of s_next.
+    // Returns this lane's raw row max of s_next.
+    auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
+                    const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
+                    unsigned char* kl_dst, bool vl_do, int vl_key0,
+                    unsigned char* vl_dst) -> float {
+        constexpr int kAhead = 3;
+        constexpr int kMma = 32;  // MFMAs per phase
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        frag p[4];
+        frag fk[kMma];
+        frag fv[kMma];
+        s_next[0] = f32x16{};
+        s_next[1] = f32x16{};
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) fk[k] = k_frag(kt, k);
+#pragma unroll
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fk[i + kAhead] = k_frag(kt, i + kAhead);
+            else fv[i + kAhead - kMma] = v_frag(vt, i + kAhead - kMma);
+            s_next[i >> 4] = Elem<T>::mma(fk[i], qf[i & 15], s_next[i >> 4]);
+            // Load slots: MFMAs 1, 3, 5, ...: K parts in the first half, V parts in the second.
+            if (i & 1) {
+                const int slot = (i & 15) >> 1;  // 0..7
+                if (slot < kParts) {
+                    if (i < 16 && kl_do) load_part(Kh, kl_key0, kl_dst, slot);
+                    if (i >= 16 && vl_do) load_part(Vh, vl_key0, vl_dst, slot);
+                }
+            } else {
+                exp_one(s, 0, i >> 1, m_use);
+            }
+            if ((i & 15) == 14) p[i >> 4] = pack_p(s, 0, i >> 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
+        float mx = -INFINITY;
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fv[i + kAhead] = v_frag(vt, i + kAhead);
+            o[i & 7] = Elem<T>::mma(fv[i], p[i >> 3], o[i & 7]);
+            if (i < 16) {
+                exp_one(s, 1, i, m_use);
+                if ((i & 7) == 7) p[2 + (i >> 3)] = pack_p(s, 1, i >> 3);
+            }
+            // Row sum of the fp32 exponentials (tile 0 in MFMAs 0-15, tile 1 in 16-31).
+            sum += s[i >> 4][i & 15];
+            mx = __builtin_elementwise_maximum(mx, s_next[i >> 4][i & 15]);
+            // Keep both chains here: left alone, the compiler sinks them to their first use.
+            asm volatile("" : "+v"(sum), "+v"(mx));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l += sum;
+        return mx;
+    };
+
+    // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
+    // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
+    // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
+    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and their row max (for the
+    // last block they come from a stale buffer and the max is replaced by -inf, which leaves
+    // (m, l) unchanged). The loop is unrolled by two so that every buffer is a distinct LDS
+    // object.
+    load_tile(Kh, 0, Kb0);
+    load_tile(Vh, 0, Vb0);
+    if (nkb > 1) load_tile(Kh, BN, Kb1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    f32x16 sa[2], sb[2];
+    float alpha;
+    scores(Kb0, sa);
+    if (needs_mask(0)) mask_scores(sa, 0);
+    {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
+        }
+        update_max(mx, alpha);  // O is still zero: nothing to rescale
+    }
+    for (int j = 0; j < nkb; j += 2) {
+        // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                        j + 1 < nkb, (j + 1) * BN, Vb1);
+        if (update_max(j + 1 < nkb ? mx : -INFINITY, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+        if (j + 1 >= nkb) break;
+        // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
+                  j + 2 < nkb, (j + 2) * BN, Vb0);
+        if (update_max(j + 2 < nkb ? mx : -INFINITY, alpha)) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+    }
+
+    // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
+    l = pair_sum(l);
+    if (q < Nq) {
+        const float inv = 1.0f / l;
+        uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                u32x2 w;
+                w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
+                w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
+                st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // fp16 / bf16 kernel for head_dim 64
 // ------------------------------------------------------------------------------------------
 // fwd16_d128_kernel's data path and pipeline at head_dim 64 (config 2's shape): 64-key blocks
@@ -999,7 +1296,11 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     using Cfg = dev::Fwd16Cfg<D>;
     constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
     constexpr int kWaves64 = 8;   // waves per workgroup of the head_dim 64 kernel
-    constexpr int BM = D == 128 ? 32 * kWaves128 : D == 64 ? 32 * kWaves64 : Cfg::BM;
+    constexpr int kWaves256 = 4;  // waves per workgroup of the head_dim 256 kernel
+    constexpr int BM = D == 128 ? 32 * kWaves128
+                       : D == 64 ? 32 * kWaves64
+                       : D == 256 ? 32 * kWaves256
+                                  : Cfg::BM;
     const int nqb = (sh.Nq + BM - 1) / BM;
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
@@ -1008,6 +1309,14 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     if constexpr (D == 64) {
         hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves64>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0, stream,
+                           reinterpret_cast<const uint16_t*>(Q),
+                           reinterpret_cast<const uint16_t*>(K),
+                           reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
+                           L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
+                           causal ? 1 : 0);
+    } else if constexpr (D == 256) {
+        hipLaunchKernelGGL((dev::fwd16_d256_kernel<T, kWaves256>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves256), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
