@@ -18,7 +18,7 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
-// For fp16/bf16 at head_dim 128 and 64 the same steps run as delta_ld_kernel, then dq_lds_tiles
+// For fp16/bf16 at head_dim 64, 128 and 256 the same steps run as delta_ld_kernel, then dq_lds_tiles
 // and dkdv_lds_tiles items in one launch (bwd_fused_kernel, section 4). Every path is
 // deterministic: no atomics, and each output element is written by exactly one lane.
 //
@@ -453,7 +453,7 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// 4. Backward for head_dim 128 and 64 (fp16 / bf16)
+// 4. Backward for head_dim 64, 128 and 256 (fp16 / bf16)
 // ------------------------------------------------------------------------------------------
 // Row statistics for bwd_fused_kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
@@ -492,13 +492,15 @@ __global__ void __launch_bounds__(256)
 // dV^T += dO^T P /
 // dK^T += Q^T dS / dQ^T += K^T dS^T without bank conflicts; blocks are double-buffered with one
 // barrier per block; (L log2 e, D) rows come padded from delta_ld_kernel; and the register
-// budget allows two workgroups per CU, so the two waves of each SIMD hide each other's
-// latencies.
+// budget allows two workgroups per CU at head_dim 64 and 128, so the two waves of each SIMD hide
+// each other's latencies (one at head_dim 256).
 // LDS layout of a 16-bit tile with D-element rows, as in the forward kernels: rows in groups
-// filled by one 1 KB load instruction each (lane i writes the group's 16-byte slot i).
+// filled by 1 KB load instructions (lane i writes the 16-byte slot i of its kilobyte).
 //   D = 128 (fwd16_d128_kernel): 4-row groups of 1088 bytes, chunk c of row r at 16 (4 c + r).
 //   D = 64 (fwd16_d64_kernel): 8-row groups of 1152 bytes, chunk c of row r at
 //            16 (8 c + (r ^ 4 ((c >> 1) & 1))).
+//   D = 256 (fwd16_d256_kernel): 4-row groups of 2112 bytes, two 1 KB column halves laid out
+//            as the D = 128 groups.
 // Both serve conflict-free row reads (A operands of 32 rows x 16 k) and transpose reads
 // (A operands whose k runs down 16 rows) with per-lane offsets and immediates.
 template <int D>
@@ -507,14 +509,15 @@ template <>
 struct TileGroups<128> {
     static constexpr int kRows = 4;        // rows per group
     static constexpr int kBytes = 1088;    // bytes per group
-    static constexpr int kKStep = 128;     // row reads: bytes per 16-column k-step
+    static constexpr int kHalves = 1;      // 1 KB load instructions per group
     static constexpr int kTrRows16 = 4 * kBytes;  // transpose reads: 16 rows further
     static constexpr int kTrHigh = 2 * kBytes;    // second read of a transpose operand (+8 rows)
-    static constexpr int kTrDTile = 256;          // transpose reads: next 32 columns
+    static constexpr int k_off(int ks) { return ks * 128; }     // row reads: k-step ks
+    static constexpr int dtile_off(int dt) { return dt * 256; }  // transpose reads: 32 columns
     __device__ static int ld_row(int lane) { return lane & 3; }
     __device__ static int ld_col(int lane) { return (lane >> 2) * 8; }
     // Row reads, k-step ks: this lane's 16 bytes (row lane % 32, chunk 2 ks + lane / 32) sit at
-    // row_base(lane, ks & 1) + ks * kKStep.
+    // row_base(lane, ks & 1) + k_off(ks).
     __device__ static int row_base(int lane, int) {
         return ((lane & 31) >> 2) * kBytes + (lane >> 5) * 64 + (lane & 3) * 16;
     }
@@ -527,13 +530,31 @@ struct TileGroups<128> {
     }
 };
 template <>
+struct TileGroups<256> : TileGroups<128> {
+    static constexpr int kBytes = 2 * 1024 + 64;
+    static constexpr int kHalves = 2;
+    static constexpr int kTrRows16 = 4 * kBytes;
+    static constexpr int kTrHigh = 2 * kBytes;
+    static constexpr int k_off(int ks) { return (ks >> 3) * 1024 + (ks & 7) * 128; }
+    static constexpr int dtile_off(int dt) { return (dt >> 2) * 1024 + (dt & 3) * 256; }
+    __device__ static int row_base(int lane, int) {
+        return ((lane & 31) >> 2) * kBytes + (lane >> 5) * 64 + (lane & 3) * 16;
+    }
+    __device__ static int tr_off(int lane) {
+        const int kq = lane & 15;
+        return (lane >> 5) * kBytes + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 +
+               (kq >> 2) * 16 + (kq & 1) * 8;
+    }
+};
+template <>
 struct TileGroups<64> {
     static constexpr int kRows = 8;
     static constexpr int kBytes = 1152;
-    static constexpr int kKStep = 256;
+    static constexpr int kHalves = 1;
     static constexpr int kTrRows16 = 2 * kBytes;
     static constexpr int kTrHigh = kBytes;
-    static constexpr int kTrDTile = 512;
+    static constexpr int k_off(int ks) { return ks * 256; }
+    static constexpr int dtile_off(int dt) { return dt * 512; }
     __device__ static int ld_row(int lane) { return (lane & 7) ^ (4 * ((lane >> 4) & 1)); }
     __device__ static int ld_col(int lane) { return (lane >> 3) * 8; }
     __device__ static int row_base(int lane, int odd) {
@@ -573,8 +594,8 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
     constexpr int GRP = G::kBytes;
     constexpr int QT = (BM / G::kRows) * GRP;
     constexpr int SET = 2 * QT + BM * 8;  // Q tile, dO tile, 32 x (L, D)
-    constexpr int kGroupsPerWave = BM / G::kRows / 4;  // of each 32-row tile
-    constexpr int NDT = D / 32;                        // 32-column tiles of dK, dV
+    constexpr int kLoadsPerWave = BM / G::kRows * G::kHalves / 4;  // per 32-row tile
+    constexpr int NDT = D / 32;                                   // 32-column tiles of dK, dV
     static_assert(2 * SET == dkdv_lds<D>(), "LDS size");
     using frag = typename Elem<T>::frag;
 
@@ -627,11 +648,14 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
         unsigned char* set = smem + b * SET;
 #pragma unroll
-        for (int i = 0; i < kGroupsPerWave; ++i) {
-            const int grp = wave + 4 * i;
+        for (int i = 0; i < kLoadsPerWave; ++i) {
+            const int grp = wave + 4 * (i / G::kHalves);
+            const int half = i % G::kHalves;
             const int row = min(r0 + G::kRows * grp + ld_row, Nq - 1);
-            lds_dma16_async(Qh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
-            lds_dma16_async(Oh + static_cast<size_t>(row) * D + ld_col, set + QT + grp * GRP);
+            const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
+            const int dst = grp * GRP + half * 1024;
+            lds_dma16_async(Qh + src, set + dst);
+            lds_dma16_async(Oh + src, set + QT + dst);
         }
         if (wave == 3) lds_dma4_async(LDh + 2 * r0 + lane, set + 2 * QT);
     };
@@ -668,7 +692,7 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
             frag fa[kMma];
             auto operand = [&](int k) {
                 const int ks = k >> 1;
-                return as_frag<T>(ld16((k & 1 ? ot : qt) + row_base[ks & 1] + ks * G::kKStep));
+                return as_frag<T>(ld16((k & 1 ? ot : qt) + row_base[ks & 1] + G::k_off(ks)));
             };
 #pragma unroll
             for (int i = 0; i < kMma; ++i) {
@@ -726,7 +750,7 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
             auto operand = [&](int i) {
                 const unsigned char* a = (i & 1 ? qt : ot) + tr_off +
                                          (i / (2 * NDT)) * G::kTrRows16 +
-                                         ((i >> 1) % NDT) * G::kTrDTile;
+                                         G::dtile_off((i >> 1) % NDT);
                 return tr_frag_at<T>(a, a + G::kTrHigh);
             };
 #pragma unroll
@@ -806,7 +830,7 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
     constexpr int GRP = G::kBytes;
     constexpr int KT = (BN / G::kRows) * GRP;
     constexpr int SET = 2 * KT;  // K tile, V tile
-    constexpr int kGroupsPerWave = BN / G::kRows / 4;
+    constexpr int kLoadsPerWave = BN / G::kRows * G::kHalves / 4;
     constexpr int NDT = D / 32;  // 32-column tiles of dQ
     static_assert(2 * SET == dq_lds<D>(), "LDS size");
     using frag = typename Elem<T>::frag;
@@ -849,11 +873,14 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
         const int r0 = kb * BN;
         unsigned char* set = smem + b * SET;
 #pragma unroll
-        for (int i = 0; i < kGroupsPerWave; ++i) {
-            const int grp = wave + 4 * i;
+        for (int i = 0; i < kLoadsPerWave; ++i) {
+            const int grp = wave + 4 * (i / G::kHalves);
+            const int half = i % G::kHalves;
             const int row = min(r0 + G::kRows * grp + ld_row, Nk - 1);
-            lds_dma16_async(Kh + static_cast<size_t>(row) * D + ld_col, set + grp * GRP);
-            lds_dma16_async(Vh + static_cast<size_t>(row) * D + ld_col, set + KT + grp * GRP);
+            const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
+            const int dst = grp * GRP + half * 1024;
+            lds_dma16_async(Kh + src, set + dst);
+            lds_dma16_async(Vh + src, set + KT + dst);
         }
     };
     const int row_base[2] = {G::row_base(lane, 0), G::row_base(lane, 1)};
@@ -886,7 +913,7 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
             frag fa[kMma];
             auto operand = [&](int k) {
                 const int ks = k >> 1;
-                return as_frag<T>(ld16((k & 1 ? vt : kt) + row_base[ks & 1] + ks * G::kKStep));
+                return as_frag<T>(ld16((k & 1 ? vt : kt) + row_base[ks & 1] + G::k_off(ks)));
             };
 #pragma unroll
             for (int i = 0; i < kMma; ++i) {
@@ -926,7 +953,7 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
             frag fa[kMma];
             auto operand = [&](int i) {
                 const unsigned char* a =
-                    kt + tr_off + (i / NDT) * G::kTrRows16 + (i % NDT) * G::kTrDTile;
+                    kt + tr_off + (i / NDT) * G::kTrRows16 + G::dtile_off(i % NDT);
                 return tr_frag_at<T>(a, a + G::kTrHigh);
             };
 #pragma unroll
@@ -972,8 +999,15 @@ __device__ __forceinline__ int xcc_id() {
            (kNumXcd - 1);  // HW_REG_XCC_ID[3:0]
 }
 
+// Resident workgroups per CU: two, except at head_dim 256, whose dK/dV accumulators and K/V
+// operands need the registers of a whole SIMD lane.
+template <int D>
+constexpr int bwd_fused_wgs_per_cu() {
+    return D >= 256 ? 1 : 2;
+}
+
 template <typename T, int D, bool kShares>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, (bwd_fused_wgs_per_cu<D>()))
     bwd_fused_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                     const uint16_t* __restrict__ V, const float2* __restrict__ LD,
                     const uint16_t* __restrict__ dO, uint16_t* __restrict__ dQ,
@@ -1178,8 +1212,9 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
         part = static_cast<float*>(share_ws.get());
     }
 
-    // Two resident workgroups per CU take the qblocks + kblocks work items.
-    const long long pool = std::min<long long>(qblocks + kblocks, 2LL * compute_units());
+    // The resident workgroups (one or two per CU) take the qblocks + kblocks work items.
+    const long long pool = std::min<long long>(
+        qblocks + kblocks, static_cast<long long>(dev::bwd_fused_wgs_per_cu<D>()) * compute_units());
     tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
     auto kernel = shares ? dev::bwd_fused_kernel<T, D, true> : dev::bwd_fused_kernel<T, D, false>;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
@@ -1206,7 +1241,7 @@ FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* 
                                    const float* L, const T* dO, T* dQ, T* dK, T* dV,
                                    const BwdShape& sh, float scale, bool causal,
                                    hipStream_t stream) {
-    if constexpr (!std::is_same<T, float>::value && (D == 128 || D == 64))
+    if constexpr (!std::is_same<T, float>::value && (D == 128 || D == 64 || D == 256))
         return run_backward_fused<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                                 stream);
     else
