@@ -574,6 +574,13 @@ struct TileGroups<64> {
 // kShares an item is (query head, key block) (heads = BH): it runs over that query head only
 // and stores its fp32 share of dK (scaled) and dV at part[bh] and part[BH + bh] ([BH, Nk, D]
 // each), which dkdv_reduce_kernel sums over each group.
+// Whether the items store their output rows through LDS (store_rows_staged: whole contiguous
+// rows per store instruction). Not at head_dim 128, where the staging code makes the kernel
+// spill at its 256-register budget and measured no faster.
+template <int D>
+constexpr bool bwd_staged_store() {
+    return D != 128;
+}
 template <int D>
 constexpr int dkdv_lds() {  // two sets of Q tile, dO tile and 32 (L, D) rows
     return 2 * (2 * (32 / TileGroups<D>::kRows) * TileGroups<D>::kBytes + 32 * 8);
@@ -789,6 +796,15 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
                 st16(vrow + d, __builtin_bit_cast(u32x4, wv));
             }
         }
+    } else if constexpr (!kShares && bwd_staged_store<D>()) {
+        // dK and dV rows through LDS (the tile sets, free once every wave is past its last
+        // block), one after the other in the wave's area.
+        static_assert(4 * staged_rows_bytes<D>() <= dkdv_lds<D>(), "staging area");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        unsigned char* stg = smem + wave * staged_rows_bytes<D>();
+        store_rows_staged<T, D>(dk, scale, stg, dK + kv_head, k0, Nk);
+        store_rows_staged<T, D>(dv, 1.0f, stg, dV + kv_head, k0, Nk);
     } else if (!kShares && key_ok) {
         uint16_t* krow = dK + kv_head + static_cast<size_t>(key) * D;
         uint16_t* vrow = dV + kv_head + static_cast<size_t>(key) * D;
@@ -969,7 +985,14 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
         }
     }
 
-    if (q_ok) {
+    if constexpr (bwd_staged_store<D>()) {
+        // dQ rows through LDS (the tile sets, free once every wave is past its last block).
+        static_assert(4 * staged_rows_bytes<D>() <= dq_lds<D>(), "staging area");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        store_rows_staged<T, D>(acc, scale, smem + wave * staged_rows_bytes<D>(), dQ + head, q0,
+                                Nq);
+    } else if (q_ok) {
         uint16_t* row = dQ + head + static_cast<size_t>(q) * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {

@@ -136,6 +136,47 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Row-tile store through LDS. A wave holds 32 rows of a [rows, D] 16-bit output as accumulator
+// tiles (lane l: row r0 + l % 32, columns 32 dt + 8 (r / 4) + 4 (l / 32) + r % 4 of acc[dt][r]).
+// Stored straight from that layout, each 8-byte store instruction writes 16-byte pieces of 32
+// rows 2 D bytes apart. store_rows_staged instead writes the rows (times mul, RNE) to the wave's
+// LDS area stg (32 rows of 2 D + 16 bytes; the padding spreads the 32 rows over the banks) and
+// stores 1 KB of whole contiguous rows per instruction, non-temporally. Rows at or past nrows
+// are not stored. LDS accesses of one wave are performed in order, so the caller only has to
+// make sure no other wave still uses stg.
+// ---------------------------------------------------------------------------------------------
+template <int D>
+constexpr int staged_rows_bytes() {
+    return 32 * (2 * D + 16);
+}
+template <typename T, int D>
+__device__ __forceinline__ void store_rows_staged(const f32x16 (&acc)[D / 32], float mul,
+                                                  unsigned char* stg, uint16_t* base, int r0,
+                                                  int nrows) {
+    constexpr int P = 2 * D + 16;  // staging row pitch (bytes)
+    constexpr int LPR = D / 8;     // lanes per row, 16 bytes each
+    const int lane = threadIdx.x & 63;
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            u32x2 w;
+            w[0] = Elem<T>::pack2(acc[dt][4 * a + 0] * mul, acc[dt][4 * a + 1] * mul);
+            w[1] = Elem<T>::pack2(acc[dt][4 * a + 2] * mul, acc[dt][4 * a + 3] * mul);
+            st8(stg + l32 * P + (32 * dt + 8 * a + 4 * g2) * 2, w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+        const int r = (64 / LPR) * i + lane / LPR;
+        const u32x4 v = ld16(stg + r * P + (lane % LPR) * 16);
+        if (r0 + r < nrows) st16_nt(base + static_cast<size_t>(r0 + r) * D + (lane % LPR) * 8, v);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // LDS transpose read (gfx950 ds_read_b64_tr_b16).
 // Within each 16-lane group, result lane i, slot j (j = 0..3) is element i%4 of the 8-byte chunk
 // addressed by lane 4*j + i/4 of the same group (verified on gfx950). `read_tr_frag` uses it to

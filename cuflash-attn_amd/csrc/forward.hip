@@ -205,37 +205,6 @@ __global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
     }
 }
 
-// Epilogue of the pipelined kernels: stores this wave's 32 rows of O / l (rows q0 .. q0 + 31,
-// this lane's row q0 + l % 32 held as accumulator tiles o[dt]) with RNE. The tile goes through
-// the wave's LDS staging area stg (32 rows of 2 D + 16 bytes) so that each global store writes
-// 1 KB of whole contiguous rows; stored 16 bytes at a time straight from the accumulator layout,
-// every store instruction would write 16-byte pieces of 32 rows 2 D bytes apart.
-template <typename T, int D>
-__device__ __forceinline__ void store_o_staged(const f32x16 (&o)[D / 32], float inv,
-                                               unsigned char* stg, uint16_t* Oh, int q0, int Nq) {
-    constexpr int OP = 2 * D + 16;  // staging row pitch (bytes)
-    constexpr int LPR = D / 8;      // lanes per row, 16 bytes each
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31;
-    const int g2 = lane >> 5;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-            u32x2 w;
-            w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
-            w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
-            st8(stg + l32 * OP + (32 * dt + 8 * a + 4 * g2) * 2, w);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < D / 16; ++i) {
-        const int r = (64 / LPR) * i + lane / LPR;
-        const u32x4 v = ld16(stg + r * OP + (lane % LPR) * 16);
-        if (q0 + r < Nq) st16_nt(Oh + static_cast<size_t>(q0 + r) * D + (lane % LPR) * 8, v);
-    }
-}
-
 // ------------------------------------------------------------------------------------------
 // fp16 / bf16 kernel for head_dim 128 (the headline shape), software-pipelined
 // ------------------------------------------------------------------------------------------
@@ -533,13 +502,14 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert(NW == 8 && 2 * 32 * (2 * D + 16) <= TILE, "two waves' O rows per K/V buffer");
+    static_assert(NW == 8 && 2 * staged_rows_bytes<D>() <= TILE,
+                  "two waves' O rows per K/V buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    store_o_staged<T, D>(o, 1.0f / l,
-                         (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
-                             (wave & 1) * 32 * (2 * D + 16),
-                         O + head, q0, Nq);
+    store_rows_staged<T, D>(o, 1.0f / l,
+                            (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
+                                (wave & 1) * staged_rows_bytes<D>(),
+                            O + head, q0, Nq);
     if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
 }
 
@@ -824,11 +794,13 @@ __global__ void __launch_bounds__(64 * NW, 1)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert(NW == 4 && 2 * 32 * (2 * D + 16) <= TILE, "two waves' O rows per K buffer");
+    static_assert(NW == 4 && 2 * staged_rows_bytes<D>() <= TILE,
+                  "two waves' O rows per K buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    store_o_staged<T, D>(o, 1.0f / l, (wave < 2 ? Kb0 : Kb1) + (wave & 1) * 32 * (2 * D + 16),
-                         O + head, q0, Nq);
+    store_rows_staged<T, D>(o, 1.0f / l,
+                            (wave < 2 ? Kb0 : Kb1) + (wave & 1) * staged_rows_bytes<D>(),
+                            O + head, q0, Nq);
     if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
 }
 
@@ -1125,13 +1097,14 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert(NW == 8 && 2 * 32 * (2 * D + 16) <= TILE, "two waves' O rows per K/V buffer");
+    static_assert(NW == 8 && 2 * staged_rows_bytes<D>() <= TILE,
+                  "two waves' O rows per K/V buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    store_o_staged<T, D>(o, 1.0f / l,
-                         (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
-                             (wave & 1) * 32 * (2 * D + 16),
-                         O + head, q0, Nq);
+    store_rows_staged<T, D>(o, 1.0f / l,
+                            (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
+                                (wave & 1) * staged_rows_bytes<D>(),
+                            O + head, q0, Nq);
     if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
 }
 
