@@ -24,7 +24,7 @@ Before the W warmup steps the step runs untimed for --ramp-ms (default 1 s): the
 steps after the inputs are written run 5-10% slower while the GPU's clock settles.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu-baseline]
-                      [--no-decode] [--no-ext]
+                      [--no-decode] [--no-ext] [--no-configs]
 """
 
 from __future__ import annotations
@@ -41,6 +41,7 @@ sys.path.insert(0, REPO)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 (MFMA)
 
 CFG3 = dict(B=2, H=16, N=4096, D=128, causal=True)
 CFG4 = dict(B=16, H=32, LKV=32768, D=128)
@@ -115,6 +116,7 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-ext", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg3", "decode", "copy"), default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
     ap.add_argument("--cpu-seq", type=int, default=2048,
@@ -192,6 +194,87 @@ def bench_ext(lib, torch, steps, stream):
             rec["step_tflops"] = round(3.5 * f_fwd / ((k_ms["forward"] + b_ms) * 1e-3) / 1e12, 1)
         out[name] = rec
         log(f"ext {name}: {rec}")
+        del q, k, v, do, o, lse, dq, dk, dv
+        torch.cuda.empty_cache()
+    return out
+
+
+CONFIG_WORKLOADS = [
+    # name, dtype suffix, B, H, N, D, causal, backward too, input distribution
+    ("cfg1", "f32", 2, 8, 1024, 64, True, False, "uniform[-1,1]"),
+    ("cfg2", "f16", 4, 16, 2048, 64, False, False, "N(0,1)"),
+    ("cfg5", "bf16", 1, 32, 16384, 128, True, True, "N(0,0.5)"),
+]
+
+
+def bench_configs(lib, torch, steps, stream):
+    """Times BASELINE configurations 1, 2 and 5 through the reference entry points
+    (cuflash_attention_{forward,backward}_{f32,f16,bf16}): per-launch times from the event hook,
+    TFLOP/s with the reference's FLOP model, fraction of the dense peak of the compute type
+    (fp32 MFMA for config 1). Inputs are synthetic, from torch's GPU generator."""
+    dev = torch.device("cuda:0")
+    dtypes = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+    sp = stream.cuda_stream
+    out = {}
+    for name, sfx, B, H, N, D, causal, with_bwd, dist in CONFIG_WORKLOADS:
+        dt = dtypes[sfx]
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+
+        def draw():
+            if dist.startswith("uniform"):
+                x = torch.rand((B, H, N, D), device=dev, generator=gen) * 2 - 1
+            else:
+                x = torch.randn((B, H, N, D), device=dev, generator=gen)
+                if dist == "N(0,0.5)":
+                    x = x * 0.5
+            return x.to(dt)
+
+        q, k, v, do = draw(), draw(), draw(), draw()
+        o, lse = torch.empty_like(q), torch.empty((B, H, N), device=dev, dtype=torch.float32)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        scale = D ** -0.5
+        fwd = lib.fn("forward", sfx)
+        bwd = lib.fn("backward", sfx)
+
+        def run():
+            st = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H,
+                     N, D, scale, causal, sp)
+            if with_bwd:
+                st |= bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                          lse.data_ptr(), do.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                          dv.data_ptr(), B, H, N, D, scale, causal, sp)
+            if st != 0:
+                raise RuntimeError(f"{name}: library status {st}")
+
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
+        lib.profile_enable(True)
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        rep = lib.profile_report()
+        lib.profile_enable(False)
+        peak = PEAK_FP32_TFLOPS if sfx == "f32" else PEAK_BF16_TFLOPS
+        f_fwd = flops_fwd(B, H, N, D, causal)
+        suffix = f"_{sfx}_d{D}"
+        k_ms = {lab[:-len(suffix)]: tot / n for lab, (n, tot) in rep.items()
+                if lab.endswith(suffix) and n}
+        rec = {"workload": f"{sfx} {'causal' if causal else 'non-causal'} B={B} H={H} N={N} "
+                           f"D={D}, inputs {dist}",
+               "fwd_ms": round(k_ms["forward"], 4),
+               "fwd_tflops": round(f_fwd / (k_ms["forward"] * 1e-3) / 1e12, 2),
+               "peak_tflops": peak}
+        rec["fwd_frac"] = round(rec["fwd_tflops"] / peak, 4)
+        if with_bwd:
+            b_ms = sum(v2 for k2, v2 in k_ms.items() if k2.startswith("backward"))
+            rec["bwd_ms"] = round(b_ms, 4)
+            rec["bwd_tflops"] = round(2.5 * f_fwd / (b_ms * 1e-3) / 1e12, 1)
+            rec["bwd_frac"] = round(rec["bwd_tflops"] / peak, 4)
+            rec["step_tflops"] = round(3.5 * f_fwd / ((k_ms["forward"] + b_ms) * 1e-3) / 1e12, 1)
+        out[name] = rec
+        log(f"config {name}: {rec}")
         del q, k, v, do, o, lse, dq, dk, dv
         torch.cuda.empty_cache()
     return out
@@ -352,6 +435,12 @@ def main():
     if not args.no_ext:
         log("extended forward / backward workloads")
         ext = bench_ext(lib, torch, max(3, args.steps // 4), stream)
+
+    # ---------------- configs 1, 2 and 5 ----------------
+    configs = None
+    if not args.no_configs:
+        log("configurations 1, 2 and 5")
+        configs = bench_configs(lib, torch, max(3, args.steps // 4), stream)
 
     # ---------------- config 4: split-KV decode ----------------
     decode = None
@@ -524,6 +613,7 @@ def main():
         "kernel_ms": {kk: round(vv, 4) for kk, vv in k_ms.items()},
         "decode": decode,
         "ext": ext,
+        "configs": configs,
         "parity": parity,
         "cpu_baseline": cpu,
     }

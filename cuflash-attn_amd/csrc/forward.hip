@@ -1259,6 +1259,208 @@ __global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// fp32 kernel for launches with few query blocks
+// ------------------------------------------------------------------------------------------
+// fwd32_kernel gives each wave 32 query rows and walks every key block of them in one wave, so a
+// small launch is as long as its longest query block (config 1, causal B=2 H=8 N=1024: 128
+// workgroups for 256 CUs, the last block of each head 32 key blocks long). Here a workgroup
+// owns one 32-row query block and its four waves split the key blocks (wave w takes blocks
+// w, w + 4, ...; with a causal mask their counts differ by at most one). Each wave stages its
+// own K/V tiles through its LDS area (registers -> LDS, the next block's rows loaded during the
+// current block), runs the online softmax of fwd32_kernel over its blocks and ends with a
+// partial state (m_w, l_w, O_w). The partial states go through LDS and wave 0 merges them with
+// the rule of the split-KV combine (online_softmax.cuh:28-33): M = max m_w,
+// l = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / l, L = (M + log2 l) ln 2.
+template <int D>
+__global__ void __launch_bounds__(256, 2)
+    fwd32_split_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                       const float* __restrict__ V, float* __restrict__ O, float* __restrict__ L,
+                       int Nq, int Nk, int coff, int group, int nqb, int round_len, float c,
+                       int causal) {
+    static_assert(D == 32 || D == 64, "head_dim 32 and 64");
+    constexpr int BN = 32;
+    constexpr int KP = D + 4;  // rows 16 bytes apart modulo 256 bytes
+    constexpr int VP = D + 8;  // the two rows read by one instruction sit 128 bytes apart
+    constexpr int kChunks = BN * D / 4 / 64;    // 16-byte chunks per lane per tile
+    constexpr int kWaveLds = BN * (KP + VP);    // floats per wave
+    constexpr int kMerge = 32 * D + 64;         // floats per wave: O, then m and l of 32 rows
+    static_assert(kMerge <= kWaveLds, "merge area inside the wave's tile area");
+    __shared__ __attribute__((aligned(16))) float lds[4 * kWaveLds];
+
+    // Blocks of one head share an XCD (xcd_remap) and causal blocks run longest first. The
+    // whole grid is resident at once (at most two workgroups per CU), and the dispatcher fills
+    // an XCD's CUs (round_len of them) in order, round after round, so every other round is
+    // dealt in reverse: a CU then pairs a long query block with a short one.
+    int lid = xcd_remap(blockIdx.x, gridDim.x);
+    if (round_len > 0 && gridDim.x % kNumXcd == 0) {
+        const int per_xcd = gridDim.x / kNumXcd;
+        const int base = lid - lid % per_xcd;
+        const int i = lid % per_xcd;
+        const int r = i / round_len;
+        const int pos = i % round_len;
+        const int len = min(round_len, per_xcd - r * round_len);
+        lid = base + r * round_len + ((r & 1) ? len - 1 - pos : pos);
+    }
+    const int bh = lid / nqb;
+    const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const float* Kh = K + kv_head;
+    const float* Vh = V + kv_head;
+    const int q0 = qb * 32;
+    const int q = q0 + l32;
+    float* Ks = lds + wave * kWaveLds;
+    float* Vs = Ks + BN * KP;
+
+    // Q^T operand: the k index of MFMA step ks in lane half g2 is d = (D/2)*g2 + ks.
+    float qf[D / 2];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (q < Nq)
+            v = __builtin_bit_cast(f32x4, ld16(Q + head + static_cast<size_t>(q) * D +
+                                               (D / 2) * g2 + 4 * i));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) qf[4 * i + u] = v[u];
+    }
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;
+    float l = 0.0f;
+
+    const int kv_end = causal ? min(Nk, q0 + 32 + coff) : Nk;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    u32x4 kreg[kChunks];
+    u32x4 vreg[kChunks];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int id = i * 64 + lane;
+            const int row = id / (D / 4);
+            const int col = (id % (D / 4)) * 4;
+            const int key = kb * BN + row;
+            if (key < Nk) {
+                const size_t off = static_cast<size_t>(key) * D + col;
+                kreg[i] = ld16(Kh + off);
+                vreg[i] = ld16(Vh + off);
+            } else {
+                kreg[i] = u32x4{0u, 0u, 0u, 0u};
+                vreg[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    // The wave's earlier reads of its tiles precede these writes: a wave's LDS accesses are
+    // performed in order.
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int id = i * 64 + lane;
+            const int row = id / (D / 4);
+            const int col = (id % (D / 4)) * 4;
+            st16(&Ks[row * KP + col], kreg[i]);
+            st16(&Vs[row * VP + col], vreg[i]);
+        }
+    };
+
+    if (wave < nkb) fetch(wave);
+    for (int kb = wave; kb < nkb; kb += 4) {
+        stage();
+        if (kb + 4 < nkb) fetch(kb + 4);
+        const int key0 = kb * BN;
+
+        f32x16 s[1];
+        s[0] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            const f32x4 a4 = __builtin_bit_cast(f32x4, ld16(&Ks[l32 * KP + (D / 2) * g2 + 4 * i]));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) s[0] = mma_f32(a4[u], qf[4 * i + u], s[0]);
+        }
+
+        const bool masked = (key0 + BN > Nk) || (causal && key0 + BN - 1 > q0 + coff);
+        float alpha;
+        const bool rescale =
+            masked ? softmax_step<1, true>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha)
+                   : softmax_step<1, false>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha);
+        if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        }
+
+        // O^T += V^T P^T: step r contracts the two keys 8*(r/4) + 4*h + r%4 (h = lane half).
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = 8 * (r >> 2) + 4 * g2 + (r & 3);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const float a = Vs[key * VP + 32 * dt + l32];
+                o[dt] = mma_f32(a, s[0][r], o[dt]);
+            }
+        }
+    }
+
+    // Merge of the four partial states. Each wave writes O_w in its accumulator layout
+    // ([dt][r][lane]) and (m_w, l_w) of its 32 rows to the start of its own area.
+    l += xor_shuffle(l, 32);
+    __syncthreads();  // every wave is past its last tile reads
+    float* mo = lds + wave * kWaveLds;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mo[(16 * dt + r) * 64 + lane] = o[dt][r];
+    }
+    if (g2 == 0) {
+        mo[32 * D + l32] = m;
+        mo[32 * D + 32 + l32] = l;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float mw[4], a[4];
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        mw[w] = lds[w * kWaveLds + 32 * D + l32];
+        M = fmaxf(M, mw[w]);
+    }
+    float lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        a[w] = (mw[w] == -INFINITY) ? 0.0f : fast_exp2(mw[w] - M);
+        lt += a[w] * lds[w * kWaveLds + 32 * D + 32 + l32];
+    }
+    if (q < Nq) {
+        const float inv = 1.0f / lt;
+        float* Orow = O + head + static_cast<size_t>(q) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                f32x4 w4;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int r = 4 * b + u;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        acc += a[w] * lds[w * kWaveLds + (16 * dt + r) * 64 + lane];
+                    w4[u] = acc * inv;
+                }
+                st16(Orow + 32 * dt + 8 * b + 4 * g2, __builtin_bit_cast(u32x4, w4));
+            }
+        }
+        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (M + fast_log2(lt)) * kLn2;
+    }
+}
+
 }  // namespace dev
 
 namespace detail {
@@ -1335,6 +1537,21 @@ FlashAttentionError run_forward32(const float* Q, const float* K, const float* V
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int tok = profile_kernel<float, D>("forward", stream);
+    if constexpr (D <= 64) {
+        // Fewer workgroups of 128 rows than two per CU: split each 32-row block's keys over
+        // the four waves of a workgroup instead (fwd32_split_kernel).
+        if (blocks < 2LL * compute_units()) {
+            const int nqb32 = (sh.Nq + 31) / 32;
+            const long long blocks32 = static_cast<long long>(nqb32) * sh.BH;
+            if (blocks32 > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+            hipLaunchKernelGGL((dev::fwd32_split_kernel<D>), dim3(static_cast<unsigned>(blocks32)),
+                               dim3(256), 0, stream, Q, K, V, O, L, sh.Nq, sh.Nk, sh.Nk - sh.Nq,
+                               sh.group, nqb32, compute_units() / dev::kNumXcd,
+                               scale * dev::kLog2e, causal ? 1 : 0);
+            profile_end(tok, stream);
+            return from_hip(hipGetLastError());
+        }
+    }
     hipLaunchKernelGGL((dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, sh.Nq, sh.Nk,
                        sh.Nk - sh.Nq, sh.group, nqb, scale * dev::kLog2e, causal ? 1 : 0);

@@ -100,3 +100,26 @@ def test_decode_parity(torch_gpu, dtype, d, kv_len, splits):
     o_ref, l_ref = oracle.forward(q, k, v, scale, False)
     check(dtype, synth.to_numpy(o), o_ref, "O")
     check(dtype, synth.to_numpy(lse), l_ref, "L")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_fp32_both_grids(torch_gpu, d, causal):
+    """fp32 at head_dim 32/64 runs fwd32_split_kernel (key blocks split over the waves of a
+    32-row workgroup) when fewer than two 128-row workgroups per CU would run, else
+    fwd32_kernel. B*H = 128 heads of N = 520 give 640 of them (fwd32_kernel); 4 heads give 20
+    (split kernel). Two heads of each launch are checked against the oracle."""
+    for B, H in ((4, 32), (1, 4)):
+        n = 520
+        q, k, v = make_inputs((B, H, n, d), "float32", seeds=(5, 6, 7))
+        scale = d ** -0.5
+        o, lse, _ = run_forward("float32", q, k, v, scale, causal)
+        torch_gpu.cuda.synchronize()
+        o = synth.to_numpy(o)
+        lse = synth.to_numpy(lse)
+        for b, h in ((0, 0), (B - 1, H - 1)):
+            o_ref, l_ref = oracle.forward(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1],
+                                          v[b:b + 1, h:h + 1], scale, causal)
+            check("float32", o[b:b + 1, h:h + 1], o_ref, f"O B={B} H={H} head {(b, h)}")
+            check("float32", lse[b:b + 1, h:h + 1], l_ref, f"L B={B} H={H} head {(b, h)}")
