@@ -805,20 +805,24 @@ __global__ void __launch_bounds__(64 * NW, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// fp16 / bf16 kernel for head_dim 64
+// fp16 / bf16 kernel for head_dim 64 and 32
 // ------------------------------------------------------------------------------------------
 // fwd16_d128_kernel's data path and pipeline at head_dim 64 (config 2's shape): 64-key blocks
 // in LDS-DMA double buffers, one workgroup of NW waves per CU, the next block's scores formed
 // while the current block's softmax runs. A 64-element row is 128 bytes, so one load
 // instruction (64 lanes x 16 bytes) fills a group of 8 rows; the group layout is given at the
-// operand offsets below.
-template <typename T, int NW>
+// operand offsets below. At head_dim 32 a row takes the first half of its 128-byte slot (the
+// same layout, read with two k-steps per score chain and one 32-column O tile), and every
+// phase has half the MFMAs, each carrying twice the VALU work.
+template <typename T, int NW, int D>
 __global__ void __launch_bounds__(64 * NW, 8 / NW)
     fwd16_d64_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                       float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
                       float c, int causal) {
-    constexpr int D = 64;
+    static_assert(D == 64 || D == 32, "rows of at most 128 bytes");
+    constexpr int KS = D / 16;   // k-steps of a score MFMA chain
+    constexpr int NDT = D / 32;  // 32-column tiles of O
     constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
     constexpr int BN = 64;
     constexpr int kParts = 8 / NW;  // load instructions per wave per 64-row tile
@@ -864,7 +868,9 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // values; their scores are masked). Issued from inline assembly as in fwd16_d128_kernel.
     // A tile that lies inside [0, Nk) is addressed as a scalar base plus a fixed per-lane offset.
     const int ld_row = (lane & 7) ^ (4 * ((lane >> 4) & 1));
-    const int ld_col = (lane >> 3) * 8;
+    // At head_dim 32 a row fills chunks 0-3 of its 128-byte slot; lanes 32-63 load the same
+    // chunks again into the unused slots 4-7.
+    const int ld_col = ((lane >> 3) % (D / 8)) * 8;
     const unsigned ld_voff = static_cast<unsigned>(((8 * wave + ld_row) * D + ld_col) * 2);
     // Part i (0..kParts-1) of a tile load: this wave's group wave + NW i.
     auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
@@ -947,10 +953,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Operand fragment i of the score MFMAs (K rows of tile half i / 4, k-step i % 4) and of
     // the P V MFMAs (V^T for key group i / 2 and d tile i % 2).
     auto k_frag = [&](const unsigned char* kt, int i) {
-        return as_frag<T>(ld16(k_addr(kt, i >> 2, i & 3)));
+        return as_frag<T>(ld16(k_addr(kt, i / KS, i % KS)));
     };
     auto v_frag = [&](const unsigned char* vt, int i) {
-        const unsigned char* a0 = vt + v_off + 2 * (i >> 1) * GRP + (i & 1) * 512;
+        const unsigned char* a0 = vt + v_off + 2 * (i / NDT) * GRP + (i % NDT) * 512;
         return tr_frag_at<T>(a0, a0 + GRP);
     };
 
@@ -985,13 +991,19 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     //   phase B: the 8 MFMAs of O^T += V^T P^T; MFMAs 0-3 carry the exponentials of tile 1
     //            (P groups 2 and 3, first used by MFMAs 4 and 6), every MFMA four terms of the
     //            fp32 row sum and the max of four scores of s_next.
+    // At head_dim 32 each phase has 4 MFMAs: phase A four exponentials per MFMA, the V load part
+    // after MFMA 3; phase B eight exponentials in each of MFMAs 0-1 and eight row-sum / max terms
+    // per MFMA.
     // Returns this lane's raw row max of s_next.
     auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
                     const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
                     unsigned char* kl_dst, bool vl_do, int vl_key0,
                     unsigned char* vl_dst) -> float {
         constexpr int kAhead = 3;
-        constexpr int kMma = 8;  // MFMAs per phase
+        constexpr int kMma = 4 * NDT;  // MFMAs per phase (8 at head_dim 64, 4 at 32)
+        constexpr int kExpA = 16 / kMma;        // tile-0 exponentials per phase-A MFMA
+        constexpr int kExpB = 16 / (kMma / 2);  // tile-1 exponentials per early phase-B MFMA
+        constexpr int kQuads = 8 / kMma;        // 4-term row sum / max groups per phase-B MFMA
         const float m_use = (m == -INFINITY) ? 0.0f : m;
         frag p[4];
         frag fk[kMma];
@@ -1004,18 +1016,19 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
         for (int i = 0; i < kMma; ++i) {
             if (i + kAhead < kMma) fk[i + kAhead] = k_frag(kt, i + kAhead);
             else fv[i + kAhead - kMma] = v_frag(vt, i + kAhead - kMma);
-            s_next[i >> 2] = Elem<T>::mma(fk[i], qf[i & 3], s_next[i >> 2]);
+            s_next[i / KS] = Elem<T>::mma(fk[i], qf[i % KS], s_next[i / KS]);
             if (i == 1 && kl_do) {
 #pragma unroll
                 for (int part = 0; part < kParts; ++part) load_part(Kh, kl_key0, kl_dst, part);
             }
-            if (i == 5 && vl_do) {
+            if (i == kMma / 2 + 1 && vl_do) {
 #pragma unroll
                 for (int part = 0; part < kParts; ++part) load_part(Vh, vl_key0, vl_dst, part);
             }
-            exp_one(s, 0, 2 * i, m_use);
-            exp_one(s, 0, 2 * i + 1, m_use);
-            if ((i & 3) == 3) p[i >> 2] = pack_p(s, 0, i >> 2);
+#pragma unroll
+            for (int e = 0; e < kExpA; ++e) exp_one(s, 0, kExpA * i + e, m_use);
+            if ((i + 1) * kExpA % 8 == 0)
+                p[(i + 1) * kExpA / 8 - 1] = pack_p(s, 0, (i + 1) * kExpA / 8 - 1);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
@@ -1024,21 +1037,26 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 #pragma unroll
         for (int i = 0; i < kMma; ++i) {
             if (i + kAhead < kMma) fv[i + kAhead] = v_frag(vt, i + kAhead);
-            o[i & 1] = Elem<T>::mma(fv[i], p[i >> 1], o[i & 1]);
-            if (i < 4) {
+            o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
+            if (i < kMma / 2) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) exp_one(s, 1, 4 * i + e, m_use);
-                if (i & 1) p[2 + (i >> 1)] = pack_p(s, 1, i >> 1);
+                for (int e = 0; e < kExpB; ++e) exp_one(s, 1, kExpB * i + e, m_use);
+                if ((i + 1) * kExpB % 8 == 0)
+                    p[2 + (i + 1) * kExpB / 8 - 1] = pack_p(s, 1, (i + 1) * kExpB / 8 - 1);
             }
-            // Row sum of the fp32 exponentials (tile 0 in MFMAs 0-3, tile 1 in MFMAs 4-7).
-            const int t = i >> 2;
-            const int r = 4 * (i & 3);
-            sum += (s[t][r] + s[t][r + 1]) + (s[t][r + 2] + s[t][r + 3]);
-            mx = __builtin_elementwise_maximum(
-                __builtin_elementwise_maximum(mx, s_next[t][r]),
-                __builtin_elementwise_maximum(s_next[t][r + 1],
-                                              __builtin_elementwise_maximum(s_next[t][r + 2],
-                                                                            s_next[t][r + 3])));
+            // Row sum of the fp32 exponentials and row max of s_next, four terms per group
+            // (tile 0 in the first half of the MFMAs, tile 1 in the second).
+#pragma unroll
+            for (int g = 0; g < kQuads; ++g) {
+                const int t = (kQuads * i + g) >> 2;
+                const int r = 4 * ((kQuads * i + g) & 3);
+                sum += (s[t][r] + s[t][r + 1]) + (s[t][r + 2] + s[t][r + 3]);
+                mx = __builtin_elementwise_maximum(
+                    __builtin_elementwise_maximum(mx, s_next[t][r]),
+                    __builtin_elementwise_maximum(
+                        s_next[t][r + 1],
+                        __builtin_elementwise_maximum(s_next[t][r + 2], s_next[t][r + 3])));
+            }
             // Keep both chains here: left alone, the compiler sinks them to their first use.
             asm volatile("" : "+v"(sum), "+v"(mx));
             __builtin_amdgcn_sched_barrier(0);
@@ -1097,7 +1115,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert(NW == 8 && 2 * staged_rows_bytes<D>() <= TILE,
+    static_assert((NW == 8 || NW == 4) && 2 * staged_rows_bytes<D>() <= TILE,
                   "two waves' O rows per K/V buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -1482,9 +1500,11 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     using Cfg = dev::Fwd16Cfg<D>;
     constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
     constexpr int kWaves64 = 8;   // waves per workgroup of the head_dim 64 kernel
+    constexpr int kWaves32 = 4;   // ... at head_dim 32 (two workgroups per CU)
     constexpr int kWaves256 = 4;  // waves per workgroup of the head_dim 256 kernel
     constexpr int BM = D == 128 ? 32 * kWaves128
                        : D == 64 ? 32 * kWaves64
+                       : D == 32 ? 32 * kWaves32
                        : D == 256 ? 32 * kWaves256
                                   : Cfg::BM;
     const int nqb = (sh.Nq + BM - 1) / BM;
@@ -1492,9 +1512,10 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int coff = sh.Nk - sh.Nq;
     const int tok = profile_kernel<T, D>("forward", stream);
-    if constexpr (D == 64) {
-        hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves64>),
-                           dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0, stream,
+    if constexpr (D == 64 || D == 32) {
+        constexpr int NW = D == 64 ? kWaves64 : kWaves32;
+        hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, NW, D>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
