@@ -18,8 +18,8 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
-// For fp16/bf16 at head_dim 64, 128 and 256 the same steps run as delta_ld_kernel, then dq_lds_tiles
-// and dkdv_lds_tiles items in one launch (bwd_fused_kernel, section 4). Every path is
+// For fp16/bf16 at head_dim 32, 64, 128 and 256 the same steps run as delta_ld_kernel, then
+// dq_lds_tiles and dkdv_lds_tiles items in one launch (bwd_fused_kernel, section 4). Every path is
 // deterministic: no atomics, and each output element is written by exactly one lane.
 //
 // Shapes: Q, O, dO, dQ are [BH, Nq, D], K, V, dK, dV are [BH / group, Nk, D] (query head bh
@@ -567,6 +567,13 @@ struct TileGroups<64> {
                (kq & 1) * 8;
     }
 };
+// head_dim 32: the head_dim-64 layout with each 64-byte row in the first half of its 128-byte
+// slot (operand reads touch chunks 0-3 only); lanes 32-63 of a load read the row's four
+// chunks again into the unused slots 4-7.
+template <>
+struct TileGroups<32> : TileGroups<64> {
+    __device__ static int ld_col(int lane) { return ((lane >> 3) & 3) * 8; }
+};
 
 // Key-stationary part of work item `bid` of heads * nkb (kb = 0, the most work, first); smem
 // holds at least dkdv_lds<D>() bytes. Without kShares an item is (key/value head, key block) and runs
@@ -696,6 +703,7 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         {
             constexpr int kAhead = 3;
             constexpr int kMma = 2 * (D / 16);
+            static_assert(kAhead <= kMma, "operands read ahead within the chain");
             frag fa[kMma];
             auto operand = [&](int k) {
                 const int ks = k >> 1;
@@ -753,6 +761,7 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         {
             constexpr int kAhead = 3;
             constexpr int kMma = 4 * NDT;  // (dV, dK) x 2 query halves x NDT column tiles
+            static_assert(kAhead <= kMma, "operands read ahead within the chain");
             frag fa[kMma];
             auto operand = [&](int i) {
                 const unsigned char* a = (i & 1 ? qt : ot) + tr_off +
@@ -926,6 +935,7 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
         {
             constexpr int kAhead = 3;
             constexpr int kMma = 2 * (D / 16);
+            static_assert(kAhead <= kMma, "operands read ahead within the chain");
             frag fa[kMma];
             auto operand = [&](int k) {
                 const int ks = k >> 1;
@@ -964,8 +974,8 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
             for (int j = 0; j < 2; ++j)
                 bsf[j] = pack_frag<T>(s[8 * j + 0], s[8 * j + 1], s[8 * j + 2], s[8 * j + 3],
                                       s[8 * j + 4], s[8 * j + 5], s[8 * j + 6], s[8 * j + 7]);
-            constexpr int kAhead = 3;
             constexpr int kMma = 2 * NDT;  // 2 key halves x NDT column tiles
+            constexpr int kAhead = kMma < 3 ? kMma : 3;  // 2 MFMAs at head_dim 32
             frag fa[kMma];
             auto operand = [&](int i) {
                 const unsigned char* a =
@@ -1264,7 +1274,8 @@ FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* 
                                    const float* L, const T* dO, T* dQ, T* dK, T* dV,
                                    const BwdShape& sh, float scale, bool causal,
                                    hipStream_t stream) {
-    if constexpr (!std::is_same<T, float>::value && (D == 128 || D == 64 || D == 256))
+    if constexpr (!std::is_same<T, float>::value &&
+                  (D == 128 || D == 64 || D == 256 || D == 32))
         return run_backward_fused<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                                 stream);
     else

@@ -696,6 +696,7 @@ __global__ void __launch_bounds__(64 * NW, 1)
                     unsigned char* vl_dst) -> float {
         constexpr int kAhead = 3;
         constexpr int kMma = 32;  // MFMAs per phase
+        static_assert(kAhead <= kMma, "operands read ahead within the chain");
         const float m_use = (m == -INFINITY) ? 0.0f : m;
         frag p[4];
         frag fk[kMma];
@@ -1001,6 +1002,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                     unsigned char* vl_dst) -> float {
         constexpr int kAhead = 3;
         constexpr int kMma = 4 * NDT;  // MFMAs per phase (8 at head_dim 64, 4 at 32)
+        static_assert(kAhead <= kMma, "operands read ahead within the chain");
         constexpr int kExpA = 16 / kMma;        // tile-0 exponentials per phase-A MFMA
         constexpr int kExpB = 16 / (kMma / 2);  // tile-1 exponentials per early phase-B MFMA
         constexpr int kQuads = 8 / kMma;        // 4-term row sum / max groups per phase-B MFMA
