@@ -18,7 +18,7 @@
 //   dkdv_kernel S = Q K^T, dP = dO V^T (lane = key),       dV^T += dO^T P, dK^T += Q^T dS
 // so each lane owns one query row of dQ, or one key row of dK/dV, for the whole kernel. For
 // fp16/bf16 P and dS are rounded to the input type before their products (fp32 accumulate).
-// For fp16/bf16 at head_dim 32, 64, 128 and 256 the same steps run as delta_ld_kernel, then
+// For fp16/bf16 (every head_dim) the same steps run as delta_ld_kernel, then
 // dq_lds_tiles and dkdv_lds_tiles items in one launch (bwd_fused_kernel, section 4). Every path is
 // deterministic: no atomics, and each output element is written by exactly one lane.
 //
@@ -465,7 +465,8 @@ __global__ void __launch_bounds__(256)
                     const float* __restrict__ L, float2* __restrict__ LD, int N, int Npad,
                     long long rows_pad, int* __restrict__ queues) {
     if (blockIdx.x == 0 && threadIdx.x < kNumXcd) queues[threadIdx.x] = 0;
-    constexpr int LPR = D / 8;  // lanes per row
+    constexpr int CHUNKS = D / 8;                // 16-byte chunks per row
+    constexpr int LPR = delta_lanes<CHUNKS>();   // lanes per row (a power of two)
     const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     const long long prow = t / LPR;  // padded row index
     const int part = static_cast<int>(t % LPR);
@@ -473,7 +474,7 @@ __global__ void __launch_bounds__(256)
     const int r = static_cast<int>(prow % Npad);
     const bool real = prow < rows_pad && r < N;
     float s = 0.0f;
-    if (real) {
+    if (real && part < CHUNKS) {
         const size_t off = static_cast<size_t>(bh * N + r) * D + part * 8;
         s = dot16<T>(ld16(dO + off), ld16(O + off));
     }
@@ -573,6 +574,13 @@ struct TileGroups<64> {
 template <>
 struct TileGroups<32> : TileGroups<64> {
     __device__ static int ld_col(int lane) { return ((lane >> 3) & 3) * 8; }
+};
+// head_dim 96: the head_dim-128 layout with each 192-byte row in the first 12 chunks of its
+// 256-byte slot (operand reads touch chunks 0-11 only); lanes 48-63 of a load read chunks 0-3
+// again into the unused slots 12-15.
+template <>
+struct TileGroups<96> : TileGroups<128> {
+    __device__ static int ld_col(int lane) { return ((lane >> 2) % 12) * 8; }
 };
 
 // Key-stationary part of work item `bid` of heads * nkb (kb = 0, the most work, first); smem
@@ -1210,7 +1218,7 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
     float2* ld = static_cast<float2*>(ws.get());
     int* queues = reinterpret_cast<int*>(static_cast<unsigned char*>(ws.get()) + ld_bytes);
 
-    const long long dblocks = (rows_pad * (D / 8) + 255) / 256;
+    const long long dblocks = (rows_pad * dev::delta_lanes<D / 8>() + 255) / 256;
     const int nqb = (sh.Nq + 127) / 128;
     const int nkb = (sh.Nk + 127) / 128;
     // Grouped heads: one dkdv item per (query head, key block) with fp32 shares of dK, dV that a
@@ -1275,7 +1283,7 @@ FlashAttentionError run_backward_d(const T* Q, const T* K, const T* V, const T* 
                                    const BwdShape& sh, float scale, bool causal,
                                    hipStream_t stream) {
     if constexpr (!std::is_same<T, float>::value &&
-                  (D == 128 || D == 64 || D == 256 || D == 32))
+                  (D == 128 || D == 64 || D == 256 || D == 32 || D == 96))
         return run_backward_fused<T, D>(Q, K, V, O, L, dO, dQ, dK, dV, sh, scale, causal,
                                                 stream);
     else

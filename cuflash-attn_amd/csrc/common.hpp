@@ -154,7 +154,8 @@ __device__ __forceinline__ void store_rows_staged(const f32x16 (&acc)[D / 32], f
                                                   unsigned char* stg, uint16_t* base, int r0,
                                                   int nrows) {
     constexpr int P = 2 * D + 16;  // staging row pitch (bytes)
-    constexpr int LPR = D / 8;     // lanes per row, 16 bytes each
+    constexpr int LPR = D / 8;     // 16-byte chunks per row
+    static_assert(D % 32 == 0, "whole 32-column accumulator tiles");
     const int lane = threadIdx.x & 63;
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
@@ -168,11 +169,13 @@ __device__ __forceinline__ void store_rows_staged(const f32x16 (&acc)[D / 32], f
             st8(stg + l32 * P + (32 * dt + 8 * a + 4 * g2) * 2, w);
         }
     }
+    // 16-byte chunk 64 i + lane of the 32 rows (LPR per row, 32 LPR = 64 (D / 16) in all).
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
-        const int r = (64 / LPR) * i + lane / LPR;
-        const u32x4 v = ld16(stg + r * P + (lane % LPR) * 16);
-        if (r0 + r < nrows) st16_nt(base + static_cast<size_t>(r0 + r) * D + (lane % LPR) * 8, v);
+        const int r = (64 * i + lane) / LPR;
+        const int cc = (64 * i + lane) % LPR;
+        const u32x4 v = ld16(stg + r * P + cc * 16);
+        if (r0 + r < nrows) st16_nt(base + static_cast<size_t>(r0 + r) * D + cc * 8, v);
     }
 }
 
