@@ -1,23 +1,24 @@
 // FlashAttention forward for gfx950 (MI355X).
 //
 // Replaces the reference's scalar forward kernel (src/forward/flash_attention_forward_typed.cu
-// :16-152) and its WMMA kernel (src/forward/flash_attention_forward_wmma.cu:30-207) with two
-// MFMA kernels of the same math:
-//   fwd16_kernel<T, D>: fp16 / bf16 inputs on v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate.
-//                       P is rounded to T before P*V while the row sum uses the fp32 P, as in the
-//                       reference WMMA kernel (forward_wmma.cu:151-156).
-//   fwd32_kernel<D>:    fp32 inputs on v_mfma_f32_32x32x2f32 (full fp32 products), P kept fp32
-//                       as in the reference scalar kernel (forward_typed.cu:113-129).
-// fp16 / bf16 at head_dim 128 and 64 run the software-pipelined fwd16_d128_kernel and
-// fwd16_d64_kernel (same math, LDS-DMA tiles; described at their definitions).
+// :16-152) and its WMMA kernel (src/forward/flash_attention_forward_wmma.cu:30-207) with MFMA
+// kernels of the same math:
+//   fwd16_d128_kernel, fwd16_d64_kernel, fwd16_d256_kernel: fp16 / bf16 inputs on
+//       v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate, software-pipelined with LDS-DMA tiles
+//       (head_dim 128 and 96, 64 and 32, 256; described at their definitions). P is rounded to
+//       T before P*V while the row sum uses the fp32 P, as in the reference WMMA kernel
+//       (forward_wmma.cu:151-156).
+//   fwd32_kernel<D>, fwd32_split_kernel<D>: fp32 inputs on v_mfma_f32_32x32x2f32 (full fp32
+//       products), P kept fp32 as in the reference scalar kernel (forward_typed.cu:113-129).
 //
-// Work decomposition (both kernels): one workgroup = 4 waves = 128 query rows of one
-// (batch, head); each wave owns 32 query rows. The kernel streams key/value blocks through LDS;
+// Work decomposition: each wave owns 32 query rows of one (batch, head), a workgroup 4 or 8
+// waves. The kernel streams key/value blocks through LDS;
 // per block each wave computes S^T = K Q^T (A = K tile from LDS, B = Q^T held in registers for
 // the whole kernel), runs the online softmax on the accumulator tile in place, and accumulates
 // O^T += V^T P^T (A = V tile read with LDS transpose reads, B = P straight from the score
 // registers). Each lane therefore owns one query row of O, and the softmax rescale is a per-lane
-// multiply. The next K/V block is fetched into registers while the current one is consumed.
+// multiply. The next K/V block is loaded (LDS-DMA for fp16 / bf16, through registers for fp32)
+// while the current one is consumed.
 // Causal launches process the longest query blocks first; blocks of one head share an XCD.
 //
 // Shapes: Q and O are [BH, Nq, D], K and V are [BH / group, Nk, D] (query head bh reads
@@ -34,181 +35,9 @@ namespace cuflash {
 namespace dev {
 
 // ------------------------------------------------------------------------------------------
-// fp16 / bf16 kernel
-// ------------------------------------------------------------------------------------------
-template <int D>
-struct Fwd16Cfg {
-    static constexpr int kThreads = 256;
-    static constexpr int BM = 128;  // query rows per workgroup (32 per wave)
-    static constexpr int BN = 64;   // keys per LDS block
-    // K tile pitch: consecutive rows start 16 bytes apart modulo 256 bytes, so the 16-byte row
-    // reads of an S^T operand (32 rows, same column) are bank-conflict free.
-    static constexpr int KP = D + 8;
-    // V tile pitch: consecutive rows start 64 bytes apart modulo 128 bytes, so the 8 rows x 64
-    // bytes touched by one transpose read spread evenly over the banks.
-    static constexpr int VP = ((2 * D) % 128 == 64) ? D : D + 32;
-    static constexpr int kChunksPerRow = D / 8;  // 16-byte chunks per row
-    static constexpr int kChunksPerThread = BN * kChunksPerRow / kThreads;
-    static_assert(BN * kChunksPerRow % kThreads == 0, "tile copy must divide evenly");
-};
-
-// Two workgroups per CU, except at head_dim 256 (O, Q^T and the scores need more than the
-// 256 registers per lane that two workgroups of four waves leave).
-template <int D>
-constexpr int fwd_min_waves() {
-    return D >= 256 ? 1 : 2;
-}
-
-template <typename T, int D>
-__global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
-    fwd16_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                 const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ L,
-                 int Nq, int Nk, int coff, int group, int nqb, float c, int causal) {
-    using Cfg = Fwd16Cfg<D>;
-    using frag = typename Elem<T>::frag;
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[Cfg::BN * Cfg::KP];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[Cfg::BN * Cfg::VP];
-
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = lid / nqb;
-    const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-    const int l32 = lane & 31;
-    const int g2 = lane >> 5;
-
-    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
-    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
-    const uint16_t* Qh = Q + head;
-    const uint16_t* Kh = K + kv_head;
-    const uint16_t* Vh = V + kv_head;
-
-    const int q0 = qb * Cfg::BM + wave * 32;  // first query row of this wave
-    const int q = q0 + l32;                   // query row owned by this lane
-
-    // Q^T as the B operand of S^T = K Q^T: lane holds Q[q][16*ks + 8*g2 + 0..7].
-    frag qf[D / 16];
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (q < Nq) v = ld16(Qh + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
-        qf[ks] = as_frag<T>(v);
-    }
-
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
-    float m = -INFINITY;
-    float l = 0.0f;
-
-    const int kv_end = causal ? min(Nk, (qb + 1) * Cfg::BM + coff) : Nk;
-    const int nkb = (kv_end + Cfg::BN - 1) / Cfg::BN;
-
-    u32x4 kreg[Cfg::kChunksPerThread];
-    u32x4 vreg[Cfg::kChunksPerThread];
-    auto fetch = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
-            const int id = i * Cfg::kThreads + tid;
-            const int row = id / Cfg::kChunksPerRow;
-            const int col = (id % Cfg::kChunksPerRow) * 8;
-            const int key = kb * Cfg::BN + row;
-            if (key < Nk) {
-                const size_t off = static_cast<size_t>(key) * D + col;
-                kreg[i] = ld16(Kh + off);
-                vreg[i] = ld16(Vh + off);
-            } else {
-                kreg[i] = u32x4{0u, 0u, 0u, 0u};
-                vreg[i] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    auto stage = [&]() {
-#pragma unroll
-        for (int i = 0; i < Cfg::kChunksPerThread; ++i) {
-            const int id = i * Cfg::kThreads + tid;
-            const int row = id / Cfg::kChunksPerRow;
-            const int col = (id % Cfg::kChunksPerRow) * 8;
-            st16(&Ks[row * Cfg::KP + col], kreg[i]);
-            st16(&Vs[row * Cfg::VP + col], vreg[i]);
-        }
-    };
-
-    const int tr_off = tr_lane_offset(Cfg::VP);
-    if (nkb > 0) fetch(0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        __syncthreads();  // every wave is done reading the previous block
-        stage();
-        __syncthreads();
-        if (kb + 1 < nkb) fetch(kb + 1);
-
-        const int key0 = kb * Cfg::BN;
-        // A wave whose rows all precede the block still runs it (every P is 0 there): a branch
-        // around the MFMAs would force copies of the O accumulators on every iteration.
-
-        // S^T = K Q^T for the two 32-key tiles of the block.
-        f32x16 s[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < D / 16; ++ks) {
-                const frag a =
-                    as_frag<T>(ld16(&Ks[(32 * t + l32) * Cfg::KP + 16 * ks + 8 * g2]));
-                s[t] = Elem<T>::mma(a, qf[ks], s[t]);
-            }
-        }
-
-        const bool masked = (key0 + Cfg::BN > Nk) || (causal && key0 + Cfg::BN - 1 > q0 + coff);
-        float alpha;
-        const bool rescale =
-            masked ? softmax_step<2, true>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha)
-                   : softmax_step<2, false>(s, key0, q + coff, Nk, causal != 0, c, m, l, alpha);
-        if (rescale) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
-        }
-
-        // O^T += V^T P^T in four 16-key steps.
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = j >> 1;
-            const int h = j & 1;
-            const frag p = pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2],
-                                        s[t][8 * h + 3], s[t][8 * h + 4], s[t][8 * h + 5],
-                                        s[t][8 * h + 6], s[t][8 * h + 7]);
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const frag a = read_tr_frag<T>(&Vs[16 * j * Cfg::VP + 32 * dt + tr_off], Cfg::VP);
-                o[dt] = Elem<T>::mma(a, p, o[dt]);
-            }
-        }
-    }
-
-    // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE.
-    l += xor_shuffle(l, 32);
-    if (q < Nq) {
-        const float inv = 1.0f / l;
-        uint16_t* Orow = O + head + static_cast<size_t>(q) * D;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                u32x2 w;
-                w[0] = Elem<T>::pack2(o[dt][4 * a + 0] * inv, o[dt][4 * a + 1] * inv);
-                w[1] = Elem<T>::pack2(o[dt][4 * a + 2] * inv, o[dt][4 * a + 3] * inv);
-                st8(Orow + 32 * dt + 8 * a + 4 * g2, w);
-            }
-        }
-        if (g2 == 0) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
-    }
-}
-
-// ------------------------------------------------------------------------------------------
 // fp16 / bf16 kernel for head_dim 128 (the headline shape), software-pipelined
 // ------------------------------------------------------------------------------------------
-// Same per-wave decomposition as fwd16_kernel (32 query rows per wave, S^T = K Q^T with Q^T in
+// The per-wave decomposition above (32 query rows per wave, S^T = K Q^T with Q^T in
 // registers, O^T += V^T P^T), restructured for gfx950:
 //  * a workgroup holds NW waves (32 NW query rows) and one workgroup runs per CU for NW = 8:
 //    the K/V tiles a workgroup loads are shared by all its waves, and a CU's vector memory
@@ -226,13 +55,15 @@ __global__ void __launch_bounds__(256, (fwd_min_waves<D>()))
 //  * the scores of block j+1 are formed by MFMA while the softmax of block j runs on the VALU
 //    (two score register sets), and P V of block j follows;
 //  * the lane-pair row max / sum use v_permlane32_swap instead of an LDS permute.
-template <typename T, int NW>
+template <typename T, int NW, int D>
 __global__ void __launch_bounds__(64 * NW, 8 / NW)
     fwd16_d128_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                       float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
                       float c, int causal) {
-    constexpr int D = 128;
+    static_assert(D == 128 || D == 96, "rows of at most 256 bytes, 4-row groups");
+    constexpr int KS = D / 16;   // k-steps of a score MFMA chain
+    constexpr int NDT = D / 32;  // 32-column tiles of O
     constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
     constexpr int BN = 64;
     constexpr int kParts = 16 / NW;  // load instructions per wave per 64-row tile
@@ -278,7 +109,9 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // before a tile is read and before a buffer is refilled).
     // A tile that lies inside [0, Nk) is addressed as a scalar base plus a fixed per-lane offset.
     const int ld_row = lane & 3;
-    const int ld_col = (lane >> 2) * 8;
+    // At head_dim 96 a row fills chunks 0-11 of its 256-byte slot; lanes 48-63 load chunks 0-3
+    // again into the unused slots 12-15.
+    const int ld_col = ((lane >> 2) % (D / 8)) * 8;
     const unsigned ld_voff = static_cast<unsigned>(((4 * wave + ld_row) * D + ld_col) * 2);
     // Part i (0..kParts-1) of a tile load: this wave's group wave + NW i.
     auto load_part = [&](const uint16_t* src, int key0, unsigned char* dst, int i) {
@@ -352,10 +185,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Operand fragment i of the score MFMAs (K rows of tile half i / 8, k-step i % 8) and of
     // the P V MFMAs (V^T for key group i / 4 and d tile i % 4).
     auto k_frag = [&](const unsigned char* kt, int i) {
-        return as_frag<T>(ld16(kt + k_off + 8 * (i >> 3) * GRP + (i & 7) * 128));
+        return as_frag<T>(ld16(kt + k_off + 8 * (i / KS) * GRP + (i % KS) * 128));
     };
     auto v_frag = [&](const unsigned char* vt, int i) {
-        const unsigned char* a0 = vt + v_off + 4 * (i >> 2) * GRP + (i & 3) * 256;
+        const unsigned char* a0 = vt + v_off + 4 * (i / NDT) * GRP + (i % NDT) * 256;
         return tr_frag_at<T>(a0, a0 + 2 * GRP);
     };
 
@@ -402,48 +235,66 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                     unsigned char* kl_dst, bool vl_do, int vl_key0,
                     unsigned char* vl_dst) -> float {
         constexpr int kAhead = 3;
+        constexpr int kMma = 4 * NDT;  // MFMAs per phase (16 at head_dim 128, 12 at 96)
+        static_assert(kAhead <= kMma, "operands read ahead within the chain");
+        // VALU work is dealt over the MFMAs of a phase by index ranges [n i / kMma,
+        // n (i + 1) / kMma): at head_dim 128 one tile-0 exponential per phase-A MFMA, two tile-1
+        // exponentials per MFMA of phase B's first half, one row-sum pair and one max step per
+        // phase-B MFMA.
         const float m_use = (m == -INFINITY) ? 0.0f : m;
         frag p[4];
-        frag fk[16];
-        frag fv[16];
+        frag fk[kMma];
+        frag fv[kMma];
         s_next[0] = f32x16{};
         s_next[1] = f32x16{};
 #pragma unroll
         for (int k = 0; k < kAhead; ++k) fk[k] = k_frag(kt, k);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (i + kAhead < 16) fk[i + kAhead] = k_frag(kt, i + kAhead);
-            else fv[i + kAhead - 16] = v_frag(vt, i + kAhead - 16);
-            s_next[i >> 3] = Elem<T>::mma(fk[i], qf[i & 7], s_next[i >> 3]);
-            // Load slots: every other MFMA, K parts in the first half, V parts in the second.
-            constexpr int kEvery = 4 / kParts;
-            const int slot = (i >> 1) & 3;
-            if ((i & 1) && slot % kEvery == kEvery - 1) {
-                if (i < 8 && kl_do) load_part(Kh, kl_key0, kl_dst, slot / kEvery);
-                if (i >= 8 && vl_do) load_part(Vh, vl_key0, vl_dst, slot / kEvery);
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fk[i + kAhead] = k_frag(kt, i + kAhead);
+            else fv[i + kAhead - kMma] = v_frag(vt, i + kAhead - kMma);
+            s_next[i / KS] = Elem<T>::mma(fk[i], qf[i % KS], s_next[i / KS]);
+            // Load slots: K part j after MFMA (j + 1) h / kParts - 1 of the first half (h = kMma
+            // / 2 MFMAs), V part j at the same place in the second half.
+#pragma unroll
+            for (int j = 0; j < kParts; ++j) {
+                constexpr int h = kMma / 2;
+                if (i == (j + 1) * h / kParts - 1 && kl_do) load_part(Kh, kl_key0, kl_dst, j);
+                if (i == h + (j + 1) * h / kParts - 1 && vl_do) load_part(Vh, vl_key0, vl_dst, j);
             }
-            exp_one(s, 0, i, m_use);
-            if ((i & 7) == 7) p[i >> 3] = pack_p(s, 0, i >> 3);
+#pragma unroll
+            for (int e = 16 * i / kMma; e < 16 * (i + 1) / kMma; ++e) {
+                exp_one(s, 0, e, m_use);
+                if ((e & 7) == 7) p[e >> 3] = pack_p(s, 0, e >> 3);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
         float mx = -INFINITY;
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (i + kAhead < 16) fv[i + kAhead] = v_frag(vt, i + kAhead);
-            o[i & 3] = Elem<T>::mma(fv[i], p[i >> 2], o[i & 3]);
-            if (i < 8) {
-                exp_one(s, 1, 2 * i, m_use);
-                exp_one(s, 1, 2 * i + 1, m_use);
-                if ((i & 3) == 3) p[2 + (i >> 2)] = pack_p(s, 1, i >> 2);
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fv[i + kAhead] = v_frag(vt, i + kAhead);
+            o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
+            // Tile-1 exponentials in the first half (P groups 2 and 3 are first used there by
+            // MFMA kMma / 2 and 3 kMma / 4).
+            if (i < kMma / 2) {
+#pragma unroll
+                for (int e = 32 * i / kMma; e < 32 * (i + 1) / kMma; ++e) {
+                    exp_one(s, 1, e, m_use);
+                    if ((e & 7) == 7) p[2 + (e >> 3)] = pack_p(s, 1, e >> 3);
+                }
             }
-            // Row sum of the fp32 exponentials (tile 0 in MFMAs 0-7, tile 1 in MFMAs 8-15).
-            sum += s[i >> 3][2 * (i & 7)] + s[i >> 3][2 * (i & 7) + 1];
-            const int t = i >> 3;
-            const int r = 2 * (i & 7);
-            mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, s_next[t][r]),
-                                               s_next[t][r + 1]);
+            // Row sum of the fp32 exponentials (tile 0 in the first half, tile 1 in the second)
+            // and row max of s_next, pairs k of scores.
+#pragma unroll
+            for (int kk = 16 * i / kMma; kk < 16 * (i + 1) / kMma; ++kk) {
+                const int t = kk >> 3;
+                const int r = 2 * (kk & 7);
+                sum += s[t][r] + s[t][r + 1];
+                mx = __builtin_elementwise_maximum(
+                    __builtin_elementwise_maximum(mx, s_next[t][r]), s_next[t][r + 1]);
+            }
             // Keep both chains here: left alone, the compiler sinks them to their first use.
             asm volatile("" : "+v"(sum), "+v"(mx));
             __builtin_amdgcn_sched_barrier(0);
@@ -1131,6 +982,13 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 // ------------------------------------------------------------------------------------------
 // fp32 kernel
 // ------------------------------------------------------------------------------------------
+// Two workgroups per CU, except at head_dim 256 (O, Q^T and the scores need more than the
+// 256 registers per lane that two workgroups of four waves leave).
+template <int D>
+constexpr int fwd_min_waves() {
+    return D >= 256 ? 1 : 2;
+}
+
 template <int D>
 struct Fwd32Cfg {
     static constexpr int kThreads = 256;
@@ -1499,16 +1357,14 @@ template <typename T, int D>
 FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, float* L,
                                   const FwdShape& sh, float scale, bool causal,
                                   hipStream_t stream) {
-    using Cfg = dev::Fwd16Cfg<D>;
     constexpr int kWaves128 = 8;  // waves per workgroup of the head_dim 128 kernel
     constexpr int kWaves64 = 8;   // waves per workgroup of the head_dim 64 kernel
     constexpr int kWaves32 = 4;   // ... at head_dim 32 (two workgroups per CU)
     constexpr int kWaves256 = 4;  // waves per workgroup of the head_dim 256 kernel
-    constexpr int BM = D == 128 ? 32 * kWaves128
+    constexpr int BM = (D == 128 || D == 96) ? 32 * kWaves128
                        : D == 64 ? 32 * kWaves64
                        : D == 32 ? 32 * kWaves32
-                       : D == 256 ? 32 * kWaves256
-                                  : Cfg::BM;
+                                  : 32 * kWaves256;
     const int nqb = (sh.Nq + BM - 1) / BM;
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
@@ -1531,8 +1387,8 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                            reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
                            L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
                            causal ? 1 : 0);
-    } else if constexpr (D == 128) {
-        hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128>),
+    } else if constexpr (D == 128 || D == 96) {
+        hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128, D>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
@@ -1540,12 +1396,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                            L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
                            causal ? 1 : 0);
     } else {
-        hipLaunchKernelGGL((dev::fwd16_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(Cfg::kThreads), 0, stream, reinterpret_cast<const uint16_t*>(Q),
-                           reinterpret_cast<const uint16_t*>(K),
-                           reinterpret_cast<const uint16_t*>(V), reinterpret_cast<uint16_t*>(O),
-                           L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
-                           causal ? 1 : 0);
+        static_assert(D == 32 || D == 64 || D == 96 || D == 128 || D == 256, "head_dim");
     }
     profile_end(tok, stream);
     return from_hip(hipGetLastError());
