@@ -589,6 +589,14 @@ struct TileGroups<96> : TileGroups<128> {
 // kShares an item is (query head, key block) (heads = BH): it runs over that query head only
 // and stores its fp32 share of dK (scaled) and dV at part[bh] and part[BH + bh] ([BH, Nk, D]
 // each), which dkdv_reduce_kernel sums over each group.
+// Whether the items address the tile loads of whole tiles as a scalar base plus a fixed
+// per-lane offset (no per-load VALU address arithmetic). Measured at config 3's shape: head_dim
+// 128 causal 1.5% faster, 96 5%; head_dim 256 and the head_dim-64 layout (also used at 32)
+// 0.5-2% slower, so those keep the per-lane addresses.
+template <int D>
+constexpr bool bwd_scalar_tile_base() {
+    return D == 128 || D == 96;
+}
 // Whether the items store their output rows through LDS (store_rows_staged: whole contiguous
 // rows per store instruction). Not at head_dim 128, where the staging code makes the kernel
 // spill at its 256-register budget and measured no faster.
@@ -622,7 +630,7 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
     using frag = typename Elem<T>::frag;
 
     int hi, kb;  // item head, key block
-    head_rank_order(bid, heads, hi, kb);
+    head_rank_order(__builtin_amdgcn_readfirstlane(bid), heads, hi, kb);  // wave-uniform (SGPRs)
     const int bkv = kShares ? hi / group : hi;    // key/value head
     const int bq0 = kShares ? hi : hi * group;    // first query head of the item
     const int qheads = kShares ? 1 : group;       // query heads of the item
@@ -661,6 +669,9 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
 
     const int ld_row = G::ld_row(lane);
     const int ld_col = G::ld_col(lane);
+    // Byte offset of this lane's 16 bytes in a load of group `wave` (rows from the tile's
+    // first row): the loads of whole tiles add only scalar offsets to it.
+    const unsigned ld_voff = static_cast<unsigned>(((G::kRows * wave + ld_row) * D + ld_col) * 2);
     auto load_block = [&](int it, int b) {
         const int bh = bq0 + it / span;
         const int r0 = (qb_begin + it % span) * BM;
@@ -669,15 +680,29 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         const uint16_t* Oh = dO + q_head;
         const float* LDh = reinterpret_cast<const float*>(LD + static_cast<size_t>(bh) * Npad);
         unsigned char* set = smem + b * SET;
+        if (bwd_scalar_tile_base<D>() && r0 + BM <= Nq) {
+            // Whole tile inside Q / dO: a scalar base per load, the fixed per-lane offset ld_voff.
 #pragma unroll
-        for (int i = 0; i < kLoadsPerWave; ++i) {
-            const int grp = wave + 4 * (i / G::kHalves);
-            const int half = i % G::kHalves;
-            const int row = min(r0 + G::kRows * grp + ld_row, Nq - 1);
-            const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
-            const int dst = grp * GRP + half * 1024;
-            lds_dma16_async(Qh + src, set + dst);
-            lds_dma16_async(Oh + src, set + QT + dst);
+            for (int i = 0; i < kLoadsPerWave; ++i) {
+                const int grp = wave + 4 * (i / G::kHalves);
+                const int half = i % G::kHalves;
+                const size_t sofs =
+                    static_cast<size_t>(r0 + 4 * G::kRows * (i / G::kHalves)) * D + 128 * half;
+                const int dst = grp * GRP + half * 1024;
+                lds_dma16_async_s(Qh + sofs, ld_voff, set + dst);
+                lds_dma16_async_s(Oh + sofs, ld_voff, set + QT + dst);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kLoadsPerWave; ++i) {
+                const int grp = wave + 4 * (i / G::kHalves);
+                const int half = i % G::kHalves;
+                const int row = min(r0 + G::kRows * grp + ld_row, Nq - 1);
+                const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
+                const int dst = grp * GRP + half * 1024;
+                lds_dma16_async(Qh + src, set + dst);
+                lds_dma16_async(Oh + src, set + QT + dst);
+            }
         }
         if (wave == 3) lds_dma4_async(LDh + 2 * r0 + lane, set + 2 * QT);
     };
@@ -869,7 +894,7 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
     using frag = typename Elem<T>::frag;
 
     int bh, rank;
-    head_rank_order(bid, BH, bh, rank);
+    head_rank_order(__builtin_amdgcn_readfirstlane(bid), BH, bh, rank);  // wave-uniform (SGPRs)
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -902,18 +927,33 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
 
     const int ld_row = G::ld_row(lane);
     const int ld_col = G::ld_col(lane);
+    const unsigned ld_voff = static_cast<unsigned>(((G::kRows * wave + ld_row) * D + ld_col) * 2);
     auto load_block = [&](int kb, int b) {
         const int r0 = kb * BN;
         unsigned char* set = smem + b * SET;
+        if (bwd_scalar_tile_base<D>() && r0 + BN <= Nk) {
+            // Whole tile inside K / V: a scalar base per load, the fixed per-lane offset ld_voff.
 #pragma unroll
-        for (int i = 0; i < kLoadsPerWave; ++i) {
-            const int grp = wave + 4 * (i / G::kHalves);
-            const int half = i % G::kHalves;
-            const int row = min(r0 + G::kRows * grp + ld_row, Nk - 1);
-            const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
-            const int dst = grp * GRP + half * 1024;
-            lds_dma16_async(Kh + src, set + dst);
-            lds_dma16_async(Vh + src, set + KT + dst);
+            for (int i = 0; i < kLoadsPerWave; ++i) {
+                const int grp = wave + 4 * (i / G::kHalves);
+                const int half = i % G::kHalves;
+                const size_t sofs =
+                    static_cast<size_t>(r0 + 4 * G::kRows * (i / G::kHalves)) * D + 128 * half;
+                const int dst = grp * GRP + half * 1024;
+                lds_dma16_async_s(Kh + sofs, ld_voff, set + dst);
+                lds_dma16_async_s(Vh + sofs, ld_voff, set + KT + dst);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kLoadsPerWave; ++i) {
+                const int grp = wave + 4 * (i / G::kHalves);
+                const int half = i % G::kHalves;
+                const int row = min(r0 + G::kRows * grp + ld_row, Nk - 1);
+                const size_t src = static_cast<size_t>(row) * D + 128 * half + ld_col;
+                const int dst = grp * GRP + half * 1024;
+                lds_dma16_async(Kh + src, set + dst);
+                lds_dma16_async(Vh + src, set + KT + dst);
+            }
         }
     };
     const int row_base[2] = {G::row_base(lane, 0), G::row_base(lane, 1)};
