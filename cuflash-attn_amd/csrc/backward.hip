@@ -154,14 +154,17 @@ constexpr int dq_min_waves() {
     return ((std::is_same<T, float>::value && D >= 128) || D >= 256) ? 1 : 2;
 }
 
+// Query block `bid` of `nblocks` (= BH * nqb); dq_kernel runs one per workgroup.
 template <typename T, int D>
-__global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
-    dq_kernel(const typename Mma<T>::elem* __restrict__ Q,
-              const typename Mma<T>::elem* __restrict__ K,
-              const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
-              const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
-              typename Mma<T>::elem* __restrict__ dQ, int Nq, int Nk, int coff, int group,
-              int nqb, float c, float scale, int causal) {
+__device__ __forceinline__ void dq_body(const typename Mma<T>::elem* __restrict__ Q,
+                                        const typename Mma<T>::elem* __restrict__ K,
+                                        const typename Mma<T>::elem* __restrict__ V,
+                                        const float* __restrict__ L,
+                                        const typename Mma<T>::elem* __restrict__ dO,
+                                        const float* __restrict__ Dl,
+                                        typename Mma<T>::elem* __restrict__ dQ, int Nq, int Nk,
+                                        int coff, int group, int nqb, float c, float scale,
+                                        int causal, int bid, int nblocks) {
     using M = Mma<T>;
     using E = typename M::elem;
     using frag = typename M::frag;
@@ -170,7 +173,7 @@ __global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
     __shared__ __attribute__((aligned(16))) E Kc[Cfg::BN * Cfg::CP];
     __shared__ __attribute__((aligned(16))) E Vs[Cfg::BN * Cfg::RP];
 
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int lid = xcd_remap(bid, nblocks);
     const int bh = lid / nqb;
     const int qb = causal ? nqb - 1 - lid % nqb : lid % nqb;
     const int tid = threadIdx.x;
@@ -288,14 +291,18 @@ struct DkvCfg {
     static constexpr int CP = BwdPitch<T, D>::CP;
 };
 
+// Key block `bid` of `nblocks` (= BHkv * nkb); dkdv_kernel runs one per workgroup.
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 1)
-    dkdv_kernel(const typename Mma<T>::elem* __restrict__ Q,
-                const typename Mma<T>::elem* __restrict__ K,
-                const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
-                const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
-                typename Mma<T>::elem* __restrict__ dK, typename Mma<T>::elem* __restrict__ dV,
-                int Nq, int Nk, int coff, int group, int nkb, float c, float scale, int causal) {
+__device__ __forceinline__ void dkdv_body(const typename Mma<T>::elem* __restrict__ Q,
+                                          const typename Mma<T>::elem* __restrict__ K,
+                                          const typename Mma<T>::elem* __restrict__ V,
+                                          const float* __restrict__ L,
+                                          const typename Mma<T>::elem* __restrict__ dO,
+                                          const float* __restrict__ Dl,
+                                          typename Mma<T>::elem* __restrict__ dK,
+                                          typename Mma<T>::elem* __restrict__ dV, int Nq, int Nk,
+                                          int coff, int group, int nkb, float c, float scale,
+                                          int causal, int bid, int nblocks) {
     using M = Mma<T>;
     using E = typename M::elem;
     using frag = typename M::frag;
@@ -307,7 +314,7 @@ __global__ void __launch_bounds__(256, 1)
     __shared__ __attribute__((aligned(16))) float Ls[Cfg::BM];
     __shared__ __attribute__((aligned(16))) float Ds[Cfg::BM];
 
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int lid = xcd_remap(bid, nblocks);
     const int bkv = lid / nkb;  // key/value head
     const int kb = lid % nkb;   // ascending: with a causal mask the first blocks carry the most work
     const int tid = threadIdx.x;
@@ -450,6 +457,50 @@ __global__ void __launch_bounds__(256, 1)
             }
         }
     }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256, (dq_min_waves<T, D>()))
+    dq_kernel(const typename Mma<T>::elem* __restrict__ Q,
+              const typename Mma<T>::elem* __restrict__ K,
+              const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
+              const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
+              typename Mma<T>::elem* __restrict__ dQ, int Nq, int Nk, int coff, int group,
+              int nqb, float c, float scale, int causal) {
+    dq_body<T, D>(Q, K, V, L, dO, Dl, dQ, Nq, Nk, coff, group, nqb, c, scale, causal,
+                  blockIdx.x, gridDim.x);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 1)
+    dkdv_kernel(const typename Mma<T>::elem* __restrict__ Q,
+                const typename Mma<T>::elem* __restrict__ K,
+                const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
+                const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
+                typename Mma<T>::elem* __restrict__ dK, typename Mma<T>::elem* __restrict__ dV,
+                int Nq, int Nk, int coff, int group, int nkb, float c, float scale, int causal) {
+    dkdv_body<T, D>(Q, K, V, L, dO, Dl, dK, dV, Nq, Nk, coff, group, nkb, c, scale, causal,
+                    blockIdx.x, gridDim.x);
+}
+
+// Both passes in one launch, for launches too small to fill the GPU one after the other: the
+// first n_dkdv workgroups run dkdv_body (the longer items first), the others dq_body. The two
+// bodies' LDS arrays add up; the register budget is dkdv's.
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 1)
+    dq_dkdv_kernel(const typename Mma<T>::elem* __restrict__ Q,
+                   const typename Mma<T>::elem* __restrict__ K,
+                   const typename Mma<T>::elem* __restrict__ V, const float* __restrict__ L,
+                   const typename Mma<T>::elem* __restrict__ dO, const float* __restrict__ Dl,
+                   typename Mma<T>::elem* __restrict__ dQ, typename Mma<T>::elem* __restrict__ dK,
+                   typename Mma<T>::elem* __restrict__ dV, int Nq, int Nk, int coff, int group,
+                   int nqb, int nkb, int n_dkdv, float c, float scale, int causal) {
+    if (static_cast<int>(blockIdx.x) < n_dkdv)
+        dkdv_body<T, D>(Q, K, V, L, dO, Dl, dK, dV, Nq, Nk, coff, group, nkb, c, scale, causal,
+                        blockIdx.x, n_dkdv);
+    else
+        dq_body<T, D>(Q, K, V, L, dO, Dl, dQ, Nq, Nk, coff, group, nqb, c, scale, causal,
+                      blockIdx.x - n_dkdv, gridDim.x - n_dkdv);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1211,33 +1262,44 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     if (err != FlashAttentionError::SUCCESS) return err;
 
     const float c = scale * dev::kLog2e;
-    {
-        using Cfg = dev::DqCfg<T, D>;
-        const int nqb = (sh.Nq + Cfg::BM - 1) / Cfg::BM;
-        const long long blocks = static_cast<long long>(nqb) * sh.BH;
-        if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-        tok = profile_kernel<T, D>("backward_dq", stream);
-        hipLaunchKernelGGL((dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
-                           reinterpret_cast<E*>(dQ), sh.Nq, sh.Nk, coff, sh.group, nqb, c, scale,
-                           causal ? 1 : 0);
-        profile_end(tok, stream);
-        err = from_hip(hipGetLastError());
-        if (err != FlashAttentionError::SUCCESS) return err;
+    using QCfg = dev::DqCfg<T, D>;
+    using KCfg = dev::DkvCfg<T, D>;
+    const int nqb = (sh.Nq + QCfg::BM - 1) / QCfg::BM;
+    const int nkb = (sh.Nk + KCfg::BN - 1) / KCfg::BN;
+    const long long qblocks = static_cast<long long>(nqb) * sh.BH;
+    const long long kblocks = static_cast<long long>(nkb) * BHkv;
+    if (qblocks + kblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+    // Both grids together fit in one round of workgroups: one launch, so that the dq and dkdv
+    // items run side by side instead of each half-filling the GPU in turn (up to head_dim 128:
+    // the two bodies' LDS arrays add up).
+    if constexpr (D <= 128) {
+        if (qblocks + kblocks <= compute_units()) {
+            tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
+            hipLaunchKernelGGL((dev::dq_dkdv_kernel<T, D>),
+                               dim3(static_cast<unsigned>(qblocks + kblocks)), dim3(256), 0,
+                               stream, q, k, v, L, go, delta, reinterpret_cast<E*>(dQ),
+                               reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk,
+                               coff, sh.group, nqb, nkb, static_cast<int>(kblocks), c, scale,
+                               causal ? 1 : 0);
+            profile_end(tok, stream);
+            return from_hip(hipGetLastError());
+        }
     }
-    {
-        using Cfg = dev::DkvCfg<T, D>;
-        const int nkb = (sh.Nk + Cfg::BN - 1) / Cfg::BN;
-        const long long blocks = static_cast<long long>(nkb) * BHkv;
-        if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-        tok = profile_kernel<T, D>("backward_dkdv", stream);
-        hipLaunchKernelGGL((dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(Cfg::kThreads), 0, stream, q, k, v, L, go, delta,
-                           reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk, coff,
-                           sh.group, nkb, c, scale, causal ? 1 : 0);
-        profile_end(tok, stream);
-        err = from_hip(hipGetLastError());
-    }
+    tok = profile_kernel<T, D>("backward_dq", stream);
+    hipLaunchKernelGGL((dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(qblocks)),
+                       dim3(QCfg::kThreads), 0, stream, q, k, v, L, go, delta,
+                       reinterpret_cast<E*>(dQ), sh.Nq, sh.Nk, coff, sh.group, nqb, c, scale,
+                       causal ? 1 : 0);
+    profile_end(tok, stream);
+    err = from_hip(hipGetLastError());
+    if (err != FlashAttentionError::SUCCESS) return err;
+    tok = profile_kernel<T, D>("backward_dkdv", stream);
+    hipLaunchKernelGGL((dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(kblocks)),
+                       dim3(KCfg::kThreads), 0, stream, q, k, v, L, go, delta,
+                       reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk, coff,
+                       sh.group, nkb, c, scale, causal ? 1 : 0);
+    profile_end(tok, stream);
+    err = from_hip(hipGetLastError());
     return err;
 }
 

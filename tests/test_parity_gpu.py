@@ -123,3 +123,28 @@ def test_forward_fp32_both_grids(torch_gpu, d, causal):
                                           v[b:b + 1, h:h + 1], scale, causal)
             check("float32", o[b:b + 1, h:h + 1], o_ref, f"O B={B} H={H} head {(b, h)}")
             check("float32", lse[b:b + 1, h:h + 1], l_ref, f"L B={B} H={H} head {(b, h)}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_fp32_both_launches(torch_gpu, causal):
+    """The fp32 backward runs dq and dkdv items in one launch (dq_dkdv_kernel) when both grids
+    fit in one round of workgroups, else dq_kernel then dkdv_kernel. B*H = 128 heads of N = 520
+    give 1,280 query and key blocks (two launches); 4 heads give 40 (one launch). Two heads of
+    each are checked against the oracle."""
+    d = 64
+    for B, H in ((4, 32), (1, 4)):
+        n = 520
+        q, k, v, do = make_inputs((B, H, n, d), "float32", seeds=(5, 6, 7, 8))
+        scale = d ** -0.5
+        o, lse, (tq, tk, tv) = run_forward("float32", q, k, v, scale, causal)
+        dq, dk, dv = cuflash_attn.flash_attention_backward(tq, tk, tv, o, lse,
+                                                           synth.to_torch(do, "float32"),
+                                                           scale=scale, causal=causal)
+        torch_gpu.cuda.synchronize()
+        got = [synth.to_numpy(x) for x in (dq, dk, dv)]
+        for b, h in ((0, 0), (B - 1, H - 1)):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            ref = oracle.backward(q[sl], k[sl], v[sl], do[sl], scale, causal)
+            for name, g, r in zip(("dQ", "dK", "dV"), got, ref):
+                check("float32", g[sl], r, f"{name} B={B} H={H} head {(b, h)}")
