@@ -148,3 +148,25 @@ def test_backward_fp32_both_launches(torch_gpu, causal):
             ref = oracle.backward(q[sl], k[sl], v[sl], do[sl], scale, causal)
             for name, g, r in zip(("dQ", "dK", "dV"), got, ref):
                 check("float32", g[sl], r, f"{name} B={B} H={H} head {(b, h)}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_forward_d64_both_workgroup_sizes(torch_gpu, dtype):
+    """head_dim 64 runs four-wave workgroups (128 rows) for non-causal launches and launches
+    with fewer eight-wave workgroups than CUs, eight-wave workgroups (256 rows) otherwise.
+    Causal B*H = 64 heads of N = 2100 take the eight-wave kernel (576 workgroups), non-causal
+    the four-wave one; two heads of each are checked against the oracle."""
+    d, n = 64, 2100
+    q, k, v = make_inputs((2, 32, n, d), dtype, seeds=(11, 12, 13), dist="normal")
+    scale = d ** -0.5
+    for causal in (True, False):
+        o, lse, _ = run_forward(dtype, q, k, v, scale, causal)
+        torch_gpu.cuda.synchronize()
+        o = synth.to_numpy(o)
+        lse = synth.to_numpy(lse)
+        for b, h in ((0, 0), (1, 31)):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            o_ref, l_ref = oracle.forward(q[sl], k[sl], v[sl], scale, causal)
+            check(dtype, o[sl], o_ref, f"O causal={causal} head {(b, h)}")
+            check(dtype, lse[sl], l_ref, f"L causal={causal} head {(b, h)}")
