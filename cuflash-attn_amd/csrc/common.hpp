@@ -72,10 +72,14 @@ struct Elem<__half> {
     static __device__ __forceinline__ float to_f(uint16_t v) {
         return static_cast<float>(__builtin_bit_cast(_Float16, v));
     }
+    // Two floats -> two RNE halves packed in one dword (low half = a): one v_cvt_pk_f16_f32.
     static __device__ __forceinline__ uint32_t pack2(float a, float b) {
-        const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
-        const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
-        return lo | (hi << 16);
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        f32x2 v;
+        v[0] = a;
+        v[1] = b;
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
     }
     static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
