@@ -1,8 +1,10 @@
 """Builds libcuflash_attn.so for gfx950 with hipcc.
 
-The shared library lands in <repo>/build/libcuflash_attn.so, one of the paths the reference's
-ctypes callers search (tests/integration/test_pytorch_comparison.py:158-180), with hidden default
+The shared library lands in <repo>/build/libcuflash_attn.so, the first path the reference's test
+caller searches (tests/integration/test_pytorch_comparison.py:158-180), with hidden default
 visibility so that only the CUFLASH_EXPORT symbols are exported (reference CMakeLists.txt:60-72).
+build/release/libcuflash_attn.so, a relative symbolic link to it, is the first path of the
+reference's example caller (examples/python_binding.py:25-48), which does not look in build/.
 
 Usage: python cuflash-attn_amd/build.py [--jobs N] [--install PREFIX]
 
@@ -28,6 +30,8 @@ INCLUDE = os.path.join(REPO_ROOT, "include")
 BUILD_DIR = os.path.join(REPO_ROOT, "build")
 LIB_NAME = "libcuflash_attn.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
+# build/release/ is where examples/python_binding.py:28 looks first (its CMake release preset).
+RELEASE_LINK = os.path.join(BUILD_DIR, "release", LIB_NAME)
 
 SOURCES = ["api.cpp", "profile.cpp", "workspace.cpp", "forward.hip", "backward.hip", "decode.hip",
            "primitives.hip"]
@@ -79,6 +83,7 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    _link_release()
     if verbose:
         print(f"built {LIB_PATH}")
     for name, src in TEST_PROGRAMS.items():
@@ -93,6 +98,17 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
         if verbose:
             print(f"built {out}")
     return LIB_PATH
+
+
+def _link_release() -> None:
+    """Points build/release/libcuflash_attn.so at ../libcuflash_attn.so (relative, so the link
+    stays valid when the tree is copied elsewhere)."""
+    os.makedirs(os.path.dirname(RELEASE_LINK), exist_ok=True)
+    tmp = RELEASE_LINK + ".tmp"
+    if os.path.lexists(tmp):
+        os.remove(tmp)
+    os.symlink(os.path.join("..", LIB_NAME), tmp)
+    os.replace(tmp, RELEASE_LINK)
 
 
 _CONFIG = """# cuflash_attn CMake package (installed by cuflash-attn_amd/build.py --install).

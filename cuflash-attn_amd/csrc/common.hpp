@@ -314,16 +314,18 @@ __device__ __forceinline__ void lds_dma16(const void* src, unsigned char* lds_ba
 // LDS and adds no waits for them, so the kernel must order every LDS access itself
 // (s_waitcnt vmcnt(0) and a barrier before the data is read, and before a buffer is reused).
 // This lets a kernel rotate buffers with run-time offsets, where the compiler would otherwise
-// wait for every outstanding load before each LDS read. An SALU write of M0 needs one wait state
-// before an LDS DMA that uses it (the s_nop); M0 has no other user in these kernels.
+// wait for every outstanding load before each LDS read. The LDS base goes in as an M0 operand
+// (constraint "{m0}"), so the compiler writes M0 itself and knows that the register is taken;
+// an SALU write of M0 needs one wait state before an LDS DMA that uses it, which the s_nop
+// inside the statement provides whatever the compiler placed in between.
 __device__ __forceinline__ unsigned lds_address(const void* p) {
     return static_cast<unsigned>(reinterpret_cast<uintptr_t>(
         (const __attribute__((address_space(3))) unsigned char*)(p)));
 }
 __device__ __forceinline__ void lds_dma16_async(const void* src, unsigned char* lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
-                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
                  : "memory");
 }
 // The same load with a wave-uniform base address in SGPRs and a 32-bit per-lane byte offset:
@@ -331,16 +333,16 @@ __device__ __forceinline__ void lds_dma16_async(const void* src, unsigned char* 
 // only advances sbase (scalar adds) from tile to tile.
 __device__ __forceinline__ void lds_dma16_async_s(const void* sbase, unsigned voff,
                                                   unsigned char* lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
                  : "v"(voff), "s"(sbase),
-                   "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                   "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
                  : "memory");
 }
 __device__ __forceinline__ void lds_dma4_async(const void* src, unsigned char* lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
                  :
-                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
                  : "memory");
 }
 

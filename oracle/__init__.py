@@ -49,8 +49,8 @@ def _load():
     lib.oracle_backward.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64,
                                     ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.oracle_backward_rows.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64,
-                                         ctypes.c_double, ctypes.c_int, _ip, _i64, _ip, _i64,
-                                         ctypes.c_int, ctypes.c_int]
+                                         _i64, ctypes.c_double, ctypes.c_int, _ip, _i64, _ip,
+                                         _i64, ctypes.c_int, ctypes.c_int]
     lib.oracle_decode_partials.argtypes = [_fp, _fp, _fp, _i64, _i64, _i64, ctypes.c_double,
                                            _i64, _i64, _dp, _dp, _dp]
     lib.oracle_decode_combine.argtypes = [_dp, _dp, _dp, _i64, _i64, _i64, _fp, _fp]
@@ -121,9 +121,15 @@ def backward(q, k, v, do, scale: float, causal: bool, nthreads: int | None = Non
 
 def backward_rows(q, k, v, do, scale: float, causal: bool, q_rows, k_rows,
                   nthreads: int | None = None, mutation: int = 0):
-    """Row-streaming gradients: dQ at q_rows [B,H,len(q_rows),D]; dK, dV at k_rows."""
+    """Row-streaming gradients: dQ at q_rows [B,H,len(q_rows),D]; dK, dV at k_rows.
+
+    K and V may have a different key count Nk than Q's Nq (causal masks j > i + Nk - Nq, as in
+    backward); q_rows index [0, Nq), k_rows index [0, Nk).
+    """
     q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
-    B, H, N, D = q.shape
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
+    assert k.shape == (B, H, Nk, D) and v.shape == k.shape and do.shape == q.shape
     qr = np.ascontiguousarray(q_rows, dtype=np.int64)
     kr = np.ascontiguousarray(k_rows, dtype=np.int64)
     dq = np.zeros((B, H, len(qr), D), dtype=np.float32)
@@ -131,7 +137,7 @@ def backward_rows(q, k, v, do, scale: float, causal: bool, q_rows, k_rows,
     dv = np.zeros((B, H, len(kr), D), dtype=np.float32)
     dummy_i = np.zeros(1, dtype=np.int64)
     rc = _load().oracle_backward_rows(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(dq), _ptr(dk), _ptr(dv), B * H, N, D,
+        _ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(dq), _ptr(dk), _ptr(dv), B * H, Nq, Nk, D,
         float(scale), int(bool(causal)), _ptr(qr if len(qr) else dummy_i), len(qr),
         _ptr(kr if len(kr) else dummy_i), len(kr), nthreads or default_threads(), mutation)
     assert rc == 0

@@ -17,7 +17,8 @@
  *                          Q and K may differ in length (Nq <= Nk when causal), as in the
  *                          forward.
  *   oracle_backward_rows   Row-streaming form of the same gradients for selected query rows
- *                          (dQ) and key rows (dK, dV), O(N*D) memory: first a pass computing
+ *                          (dQ) and key rows (dK, dV), separate query and key lengths as in
+ *                          oracle_backward, O((Nq + Nk) * D) memory: first a pass computing
  *                          L_i and O_i, then D_i = dO_i . O_i (the identity the reference kernel
  *                          uses, src/backward/flash_attention_backward_typed.cu:13-34), then
  *                          P_ij = exp(s_ij - L_i).
@@ -265,45 +266,46 @@ int oracle_backward(const float* Q, const float* K, const float* V, const float*
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* backward, row-streaming (selected rows, O(N*D) memory per head)                              */
+/* backward, row-streaming (selected rows, O((Nq + Nk) * D) memory per head)                    */
+/* Q, dO are [BH, Nq, D]; K, V are [BH, Nk, D]; causal masks j > i + Nk - Nq (as above).        */
 /* ------------------------------------------------------------------------------------------ */
 typedef struct {
     const float *Q, *K, *V, *dO;
     float *dQ, *dK, *dV;
     const i64 *qrows, *krows;
-    i64 nq, nk, BH, N, D;
+    i64 nq, nk, BH, Nq, Nk, D;
     double scale;
     int causal, mutation;
-    double *Lrow, *Drow; /* [BH][N] */
+    double *Lrow, *Drow; /* [BH][Nq] */
 } bwdr_ctx;
 
-/* pass 1: L_i and D_i = dO_i . O_i for every row of every head */
+/* pass 1: L_i and D_i = dO_i . O_i for every query row of every head */
 static void bwdr_stats(void* p, i64 begin, i64 end) {
     bwdr_ctx* c = (bwdr_ctx*)p;
-    const i64 N = c->N, D = c->D;
-    double* s = (double*)malloc(sizeof(double) * (size_t)N);
+    const i64 Nq = c->Nq, Nk = c->Nk, D = c->D;
+    double* s = (double*)malloc(sizeof(double) * (size_t)Nk);
     double* acc = (double*)malloc(sizeof(double) * (size_t)D);
     for (i64 r = begin; r < end; ++r) {
-        const i64 bh = r / N, i = r % N, off = bh * N * D;
-        const float* q = c->Q + off + i * D;
+        const i64 bh = r / Nq, i = r % Nq, qoff = bh * Nq * D, koff = bh * Nk * D;
+        const float* q = c->Q + qoff + i * D;
         double m = -INFINITY;
-        for (i64 j = 0; j < N; ++j) {
-            s[j] = masked_key(i, j, N, N, c->causal, c->mutation)
+        for (i64 j = 0; j < Nk; ++j) {
+            s[j] = masked_key(i, j, Nq, Nk, c->causal, c->mutation)
                        ? -INFINITY
-                       : score(q, c->K + off, j, D, N, c->scale, c->mutation);
+                       : score(q, c->K + koff, j, D, Nk, c->scale, c->mutation);
             if (s[j] > m) m = s[j];
         }
         const double shift = (c->mutation == 5) ? 0.0 : m;
         double l = 0.0;
         for (i64 d = 0; d < D; ++d) acc[d] = 0.0;
-        for (i64 j = 0; j < N; ++j) {
+        for (i64 j = 0; j < Nk; ++j) {
             if (s[j] == -INFINITY) continue;
             const double pj = exp(s[j] - shift);
             l += pj;
-            for (i64 d = 0; d < D; ++d) acc[d] += pj * (double)c->V[off + j * D + d];
+            for (i64 d = 0; d < D; ++d) acc[d] += pj * (double)c->V[koff + j * D + d];
         }
         double Di = 0.0;
-        for (i64 d = 0; d < D; ++d) Di += (double)c->dO[off + i * D + d] * (acc[d] / l);
+        for (i64 d = 0; d < D; ++d) Di += (double)c->dO[qoff + i * D + d] * (acc[d] / l);
         c->Lrow[r] = shift + log(l);
         c->Drow[r] = Di;
     }
@@ -311,45 +313,46 @@ static void bwdr_stats(void* p, i64 begin, i64 end) {
     free(acc);
 }
 
-/* dS_ij for one (i, j) pair given the row statistics */
-static double bwdr_ds(const bwdr_ctx* c, i64 off, i64 r0, i64 i, i64 j, double* P_out) {
-    const i64 D = c->D;
-    if (masked_key(i, j, c->N, c->N, c->causal, c->mutation)) {
+/* dS_ij of head bh for one (i, j) pair given the row statistics; P_ij in *P_out */
+static double bwdr_ds(const bwdr_ctx* c, i64 bh, i64 i, i64 j, double* P_out) {
+    const i64 D = c->D, qoff = bh * c->Nq * D, koff = bh * c->Nk * D, r = bh * c->Nq + i;
+    if (masked_key(i, j, c->Nq, c->Nk, c->causal, c->mutation)) {
         *P_out = 0.0;
         return 0.0;
     }
-    const double s = score(c->Q + off + i * D, c->K + off, j, D, c->N, c->scale, c->mutation);
-    const double P = exp(s - c->Lrow[r0 + i]);
+    const double s = score(c->Q + qoff + i * D, c->K + koff, j, D, c->Nk, c->scale, c->mutation);
+    const double P = exp(s - c->Lrow[r]);
     double dp = 0.0;
-    for (i64 d = 0; d < D; ++d) dp += (double)c->dO[off + i * D + d] * (double)c->V[off + j * D + d];
+    for (i64 d = 0; d < D; ++d) dp += (double)c->dO[qoff + i * D + d] * (double)c->V[koff + j * D + d];
     *P_out = P;
-    return P * ((c->mutation == 3) ? dp + c->Drow[r0 + i] : dp - c->Drow[r0 + i]);
+    return P * ((c->mutation == 3) ? dp + c->Drow[r] : dp - c->Drow[r]);
 }
 
 static void bwdr_grads(void* p, i64 begin, i64 end) {
     bwdr_ctx* c = (bwdr_ctx*)p;
-    const i64 N = c->N, D = c->D, per_head = c->nq + c->nk;
+    const i64 D = c->D, per_head = c->nq + c->nk;
     double* acc = (double*)malloc(sizeof(double) * (size_t)(2 * D));
     for (i64 t = begin; t < end; ++t) {
-        const i64 bh = t / per_head, w = t % per_head, off = bh * N * D, r0 = bh * N;
+        const i64 bh = t / per_head, w = t % per_head;
+        const i64 qoff = bh * c->Nq * D, koff = bh * c->Nk * D;
         double P;
         if (w < c->nq) { /* dQ row */
             const i64 i = c->qrows[w];
             for (i64 d = 0; d < D; ++d) acc[d] = 0.0;
-            for (i64 j = 0; j < N; ++j) {
-                const double ds = bwdr_ds(c, off, r0, i, j, &P);
+            for (i64 j = 0; j < c->Nk; ++j) {
+                const double ds = bwdr_ds(c, bh, i, j, &P);
                 if (ds == 0.0) continue;
-                for (i64 d = 0; d < D; ++d) acc[d] += ds * (double)c->K[off + j * D + d];
+                for (i64 d = 0; d < D; ++d) acc[d] += ds * (double)c->K[koff + j * D + d];
             }
             for (i64 d = 0; d < D; ++d) c->dQ[(bh * c->nq + w) * D + d] = (float)(acc[d] * c->scale);
         } else { /* dK, dV row */
             const i64 wk = w - c->nq, j = c->krows[wk];
             for (i64 d = 0; d < 2 * D; ++d) acc[d] = 0.0;
-            for (i64 i = 0; i < N; ++i) {
-                const double ds = bwdr_ds(c, off, r0, i, j, &P);
+            for (i64 i = 0; i < c->Nq; ++i) {
+                const double ds = bwdr_ds(c, bh, i, j, &P);
                 for (i64 d = 0; d < D; ++d) {
-                    acc[d] += ds * (double)c->Q[off + i * D + d];
-                    acc[D + d] += P * (double)c->dO[off + i * D + d];
+                    acc[d] += ds * (double)c->Q[qoff + i * D + d];
+                    acc[D + d] += P * (double)c->dO[qoff + i * D + d];
                 }
             }
             for (i64 d = 0; d < D; ++d) {
@@ -363,20 +366,25 @@ static void bwdr_grads(void* p, i64 begin, i64 end) {
 }
 
 int oracle_backward_rows(const float* Q, const float* K, const float* V, const float* dO,
-                         float* dQ, float* dK, float* dV, i64 BH, i64 N, i64 D, double scale,
-                         int causal, const i64* qrows, i64 nq, const i64* krows, i64 nk,
-                         int nthreads, int mutation) {
-    if (!Q || !K || !V || !dO || BH <= 0 || N <= 0 || D <= 0) return 1;
-    bwdr_ctx c = {Q, K, V, dO, dQ, dK, dV, qrows, krows, nq, nk, BH, N, D, scale, causal, mutation,
-                  NULL, NULL};
-    c.Lrow = (double*)malloc(sizeof(double) * (size_t)(BH * N));
-    c.Drow = (double*)malloc(sizeof(double) * (size_t)(BH * N));
+                         float* dQ, float* dK, float* dV, i64 BH, i64 Nq, i64 Nk, i64 D,
+                         double scale, int causal, const i64* qrows, i64 nq, const i64* krows,
+                         i64 nk, int nthreads, int mutation) {
+    if (!Q || !K || !V || !dO || BH <= 0 || Nq <= 0 || Nk <= 0 || D <= 0) return 1;
+    if (causal && Nq > Nk) return 1; /* rows without any visible key */
+    for (i64 w = 0; w < nq; ++w)
+        if (qrows[w] < 0 || qrows[w] >= Nq) return 1;
+    for (i64 w = 0; w < nk; ++w)
+        if (krows[w] < 0 || krows[w] >= Nk) return 1;
+    bwdr_ctx c = {Q,  K,  V,  dO, dQ, dK,    dV,     qrows,    krows, nq,  nk,
+                  BH, Nq, Nk, D,  scale, causal, mutation, NULL,  NULL};
+    c.Lrow = (double*)malloc(sizeof(double) * (size_t)(BH * Nq));
+    c.Drow = (double*)malloc(sizeof(double) * (size_t)(BH * Nq));
     if (!c.Lrow || !c.Drow) {
         free(c.Lrow);
         free(c.Drow);
         return 2;
     }
-    parallel_for(BH * N, nthreads, bwdr_stats, &c);
+    parallel_for(BH * Nq, nthreads, bwdr_stats, &c);
     parallel_for(BH * (nq + nk), nthreads, bwdr_grads, &c);
     free(c.Lrow);
     free(c.Drow);

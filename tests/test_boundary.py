@@ -299,3 +299,36 @@ def test_primitive_headers_declare_the_reference_api():
         assert "namespace kernels" in text
         for fn in fns:
             assert re.search(r"\b" + fn + r"\(", text), (header, fn)
+
+
+# The library search list of the reference's example caller (examples/python_binding.py:25-48),
+# restated as data: paths relative to the repository root that holds examples/, then the system
+# library directories. It does not look in build/ itself.
+EXAMPLE_SEARCH = ("build/release/libcuflash_attn.so", "build/debug/libcuflash_attn.so",
+                  "/usr/local/lib/libcuflash_attn.so", "/usr/lib/libcuflash_attn.so")
+
+
+def test_example_caller_search_path_finds_the_library(lib):
+    found = None
+    for p in EXAMPLE_SEARCH:
+        path = p if os.path.isabs(p) else os.path.join(REPO, p)
+        if os.path.exists(path):
+            found = path
+            break
+    assert found == os.path.join(REPO, "build", "release", "libcuflash_attn.so")
+    assert os.path.realpath(found) == os.path.realpath(lib.path)
+    handle = ctypes.CDLL(found)
+    for sym in ("cuflash_attention_forward_f32", "cuflash_attention_backward_f32",
+                "cuflash_error_string"):
+        assert getattr(handle, sym) is not None
+    handle.cuflash_error_string.restype = ctypes.c_char_p
+    assert handle.cuflash_error_string(0) == b"Success"
+
+
+def test_test_caller_search_path_finds_the_library(lib):
+    # tests/integration/test_pytorch_comparison.py:158-180 without $CUFLASH_LIB: build/ first.
+    presets = ("default", "release", "release-fast-math", "minimal", "Release", "Debug")
+    order = [os.path.join(REPO, "build", "libcuflash_attn.so")]
+    order += [os.path.join(REPO, "build", d, "libcuflash_attn.so") for d in presets]
+    first = next(p for p in order if os.path.exists(p))
+    assert first == lib.path

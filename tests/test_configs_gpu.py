@@ -77,7 +77,10 @@ def test_config2_fp16_noncausal(torch_gpu):
         assert max_abs(l_np[sl], l_ref) <= TOL16
 
 
-def _fwd_bwd_config(torch_gpu, B, H, N, D, std, heads, row_step):
+def _fwd_bwd_config(torch_gpu, B, H, N, D, std, fwd_heads, dq_heads, dkdv_heads, row_step):
+    """Forward + backward at full size. O and L are compared on `fwd_heads`; dQ on every row of
+    `dq_heads` and dK, dV on every row of `dkdv_heads` when row_step is None, else on every
+    row_step-th row plus the edge rows; every head through check_invariants."""
     scale = D ** -0.5
     host, (q, k, v, do) = gpu_inputs((B, H, N, D), "bfloat16", "normal", (1, 2, 3, 4), std)
     o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=scale, causal=True)
@@ -89,27 +92,41 @@ def _fwd_bwd_config(torch_gpu, B, H, N, D, std, heads, row_step):
         assert np.isfinite(t).all()
     check_invariants(host[0], host[1], host[2], got[0], got[1], host[3], got[2], got[3], got[4],
                      scale, n_tol=2e-2)
-    rows = np.unique(np.concatenate([np.arange(0, N, row_step), [1, 2, N - 2, N - 1]]))
-    for b, h in heads:
+    if row_step is None:
+        rows = np.arange(N)
+    else:
+        rows = np.unique(np.concatenate([np.arange(0, N, row_step), [1, 2, N - 2, N - 1]]))
+    none = np.zeros(0, dtype=np.int64)
+    for b, h in sorted(set(fwd_heads) | set(dq_heads) | set(dkdv_heads)):
         sl = (slice(b, b + 1), slice(h, h + 1))
         qh, kh, vh, doh = (x[sl] for x in host)
-        o_ref, l_ref = oracle.forward(qh, kh, vh, scale, True)
-        assert max_abs(got[0][sl], o_ref) <= TOL16
-        assert max_abs(got[1][sl], l_ref) <= TOL16
-        rq, rk, rv = oracle.backward_rows(qh, kh, vh, doh, scale, True, rows, rows)
-        assert max_abs(got[2][sl][:, :, rows], rq) <= TOL16, "dQ"
-        assert max_abs(got[3][sl][:, :, rows], rk) <= TOL16, "dK"
-        assert max_abs(got[4][sl][:, :, rows], rv) <= TOL16, "dV"
+        if (b, h) in fwd_heads:
+            o_ref, l_ref = oracle.forward(qh, kh, vh, scale, True)
+            assert max_abs(got[0][sl], o_ref) <= TOL16, f"O {(b, h)}"
+            assert max_abs(got[1][sl], l_ref) <= TOL16, f"L {(b, h)}"
+        qr = rows if (b, h) in dq_heads else none
+        kr = rows if (b, h) in dkdv_heads else none
+        rq, rk, rv = oracle.backward_rows(qh, kh, vh, doh, scale, True, qr, kr)
+        if len(qr):
+            assert max_abs(got[2][sl][:, :, qr], rq) <= TOL16, f"dQ {(b, h)}"
+        if len(kr):
+            assert max_abs(got[3][sl][:, :, kr], rk) <= TOL16, f"dK {(b, h)}"
+            assert max_abs(got[4][sl][:, :, kr], rv) <= TOL16, f"dV {(b, h)}"
 
 
 @pytest.mark.gpu
 def test_config3_bf16_causal_fwd_bwd(torch_gpu):
-    _fwd_bwd_config(torch_gpu, 2, 16, 4096, 128, 1.0, heads=((0, 0), (1, 15)), row_step=37)
+    # every row: dK and dV of four heads, dQ of two
+    heads4 = ((0, 0), (0, 9), (1, 6), (1, 15))
+    _fwd_bwd_config(torch_gpu, 2, 16, 4096, 128, 1.0, fwd_heads=heads4,
+                    dq_heads=((0, 0), (1, 15)), dkdv_heads=heads4, row_step=None)
 
 
 @pytest.mark.gpu
 def test_config5_bf16_long_context_fwd_bwd(torch_gpu):
-    _fwd_bwd_config(torch_gpu, 1, 32, 16384, 128, 0.5, heads=((0, 31),), row_step=509)
+    heads = ((0, 0), (0, 31))
+    _fwd_bwd_config(torch_gpu, 1, 32, 16384, 128, 0.5, fwd_heads=heads, dq_heads=heads,
+                    dkdv_heads=heads, row_step=127)
 
 
 @pytest.mark.gpu

@@ -236,6 +236,27 @@ def test_streaming_backward_matches_materialized(causal):
     np.testing.assert_allclose(rv, dv[:, :, rows[::-1]], atol=2e-6)
 
 
+@pytest.mark.parametrize("nq,nk,causal", [(20, 53, True), (20, 53, False), (53, 20, False),
+                                          (1, 9, True)])
+def test_streaming_backward_matches_materialized_separate_lengths(nq, nk, causal):
+    """The row-streaming form with Nq != Nk (causal mask aligned to the end of the keys) equals
+    the materialized backward, which test_separate_lengths_match_torch_float64 pins."""
+    d = 32
+    q, do = synth.normal(70, (1, 3, nq, d)), synth.normal(71, (1, 3, nq, d))
+    k, v = synth.normal(72, (1, 3, nk, d)), synth.normal(73, (1, 3, nk, d))
+    dq, dk, dv = oracle.backward(q, k, v, do, 0.2, causal)
+    qrows = np.arange(nq)
+    krows = np.arange(nk)[::-1].copy()
+    rq, rk, rv = oracle.backward_rows(q, k, v, do, 0.2, causal, qrows, krows)
+    np.testing.assert_allclose(rq, dq, atol=2e-6)
+    np.testing.assert_allclose(rk, dk[:, :, krows], atol=2e-6)
+    np.testing.assert_allclose(rv, dv[:, :, krows], atol=2e-6)
+    if causal and nq < nk:
+        # a planted top-left mask changes the gradients
+        mq, mk, _ = oracle.backward_rows(q, k, v, do, 0.2, causal, qrows, krows, mutation=7)
+        assert max(np.abs(mq - dq).max(), np.abs(mk - dk[:, :, krows]).max()) > 1e-3
+
+
 @pytest.mark.parametrize("nsplit", [1, 3, 8, 64])
 def test_split_partials_combine_to_forward_row(nsplit):
     kv_len, d = 200, 64
