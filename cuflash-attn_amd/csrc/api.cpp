@@ -444,6 +444,19 @@ int cuflash_attention_decode_f16(const __half* Q, const __half* K, const __half*
         Q, K, V, O, L, batch_size, num_heads, kv_len, head_dim, scale, num_splits, stream));
 }
 
+int cuflash_attention_decode_noalloc_f16(const __half* Q, const __half* K, const __half* V,
+                                         __half* O, float* L, int batch_size, int num_heads,
+                                         int kv_len, int head_dim, float scale, int num_splits,
+                                         hipStream_t stream) {
+    cuflash::FlashAttentionError err = cuflash::check_decode(Q, K, V, O, L, batch_size, num_heads,
+                                                             kv_len, head_dim, scale, num_splits);
+    if (err == cuflash::FlashAttentionError::SUCCESS)
+        err = cuflash::detail::launch_decode_noalloc<__half>(Q, K, V, O, L, batch_size, num_heads,
+                                                             kv_len, head_dim, scale, num_splits,
+                                                             stream);
+    return static_cast<int>(err);
+}
+
 int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const __hip_bfloat16* K,
                                   const __hip_bfloat16* V, __hip_bfloat16* O, float* L,
                                   int batch_size, int num_heads, int kv_len, int head_dim,

@@ -12,6 +12,8 @@
 // decode_combine_kernel: per (batch*head), M = max_s m_s, l = sum_s l_s 2^(m_s - M),
 //   O = sum_s acc_s 2^(m_s - M) / l, L = (M + log2 l) * ln 2.
 
+#include <mutex>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "profile.hpp"
@@ -351,9 +353,17 @@ int choose_splits(int requested, int BH, int kv_len) {
 // One decode: the layout and head grouping come in `a` (chunk and nsplit are set here).
 // Workgroups: one per (batch, key/value head, group of G query heads, split); partials and the
 // combine: one slot per (batch, query head).
+// Memory for the split partials that the caller provides instead of the stream-ordered
+// workspace (ptr == nullptr: allocate one).
+struct FixedScratch {
+    void* ptr;
+    size_t bytes;
+};
+
 template <typename T, int D, int G, bool PAGED>
 FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* L, int B,
-                               dev::DecodeArgs a, int num_splits, hipStream_t stream) {
+                               dev::DecodeArgs a, int num_splits, const FixedScratch& fixed,
+                               hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     using Cfg = dev::DecCfg<T, D>;
     const long long groups = static_cast<long long>(B) * a.Hkv * ((a.H / a.Hkv) / G);
@@ -368,10 +378,18 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     const size_t acc_bytes = static_cast<size_t>(slots) * D * sizeof(float);
     const size_t ml_bytes = static_cast<size_t>(slots) * sizeof(float2);
     StreamWorkspace ws(stream);
-    FlashAttentionError err = ws.alloc(acc_bytes + ml_bytes);
-    if (err != FlashAttentionError::SUCCESS) return err;
-    float* part_acc = static_cast<float*>(ws.get());
-    float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws.get()) + acc_bytes);
+    void* base = fixed.ptr;
+    if (base != nullptr) {
+        if (acc_bytes + ml_bytes > fixed.bytes) return FlashAttentionError::OUT_OF_MEMORY;
+    } else {
+        FlashAttentionError err = ws.alloc(acc_bytes + ml_bytes);
+        if (err != FlashAttentionError::SUCCESS) return err;
+        base = ws.get();
+    }
+    // Every (query head, split) slot is written by the split kernel before the combine kernel
+    // reads it, so neither buffer needs clearing.
+    float* part_acc = static_cast<float*>(base);
+    float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(base) + acc_bytes);
 
     int tok = profile_kernel<T, D>("decode_split", stream);
     hipLaunchKernelGGL((dev::decode_split_kernel<T, D, G, PAGED>),
@@ -379,7 +397,7 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
                        reinterpret_cast<const E*>(Q), reinterpret_cast<const E*>(K),
                        reinterpret_cast<const E*>(V), part_acc, part_ml, a);
     profile_end(tok, stream);
-    err = from_hip(hipGetLastError());
+    FlashAttentionError err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
     tok = profile_kernel<T, D>("decode_combine", stream);
     hipLaunchKernelGGL((dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(bhq)),
@@ -394,28 +412,33 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
 template <typename T, int D, bool PAGED>
 FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O, float* L, int B,
                                        const dev::DecodeArgs& a, int num_splits,
-                                       hipStream_t stream) {
+                                       const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
-    if (hpk % 8 == 0) return run_decode<T, D, 8, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
-    if (hpk % 4 == 0) return run_decode<T, D, 4, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
-    if (hpk % 2 == 0) return run_decode<T, D, 2, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
-    return run_decode<T, D, 1, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+    if (hpk % 8 == 0)
+        return run_decode<T, D, 8, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
+    if (hpk % 4 == 0)
+        return run_decode<T, D, 4, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
+    if (hpk % 2 == 0)
+        return run_decode<T, D, 2, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
+    return run_decode<T, D, 1, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
 }
 
 template <typename T, bool PAGED>
 FlashAttentionError run_decode_dims(const T* Q, const T* K, const T* V, T* O, float* L, int B,
                                     const dev::DecodeArgs& a, int head_dim, int num_splits,
-                                    hipStream_t stream) {
+                                    const FixedScratch& fx, hipStream_t stream) {
     switch (head_dim) {
         case 32:
-            return run_decode_grouped<T, 32, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+            return run_decode_grouped<T, 32, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
         case 64:
-            return run_decode_grouped<T, 64, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+            return run_decode_grouped<T, 64, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
         case 128:
-            return run_decode_grouped<T, 128, PAGED>(Q, K, V, O, L, B, a, num_splits, stream);
+            return run_decode_grouped<T, 128, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     }
     return FlashAttentionError::UNSUPPORTED_HEAD_DIM;
 }
+
+constexpr FixedScratch kAllocate{nullptr, 0};
 
 dev::DecodeArgs decode_args(int num_heads, int num_kv_heads, int kv_len, float scale) {
     dev::DecodeArgs a{};
@@ -437,7 +460,8 @@ FlashAttentionError launch_decode_gqa(const T* Q, const T* K, const T* V, T* O, 
                                       int kv_len, int head_dim, float scale, int num_splits,
                                       hipStream_t stream) {
     const dev::DecodeArgs a = decode_args(num_heads, num_kv_heads, kv_len, scale);
-    return run_decode_dims<T, false>(Q, K, V, O, L, batch_size, a, head_dim, num_splits, stream);
+    return run_decode_dims<T, false>(Q, K, V, O, L, batch_size, a, head_dim, num_splits,
+                                     kAllocate, stream);
 }
 
 template <typename T>
@@ -463,8 +487,66 @@ FlashAttentionError launch_decode_paged(const T* Q, const T* K_cache, const T* V
     a.max_pages = max_pages_per_seq;
     a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz(page_size) : -1;
     return run_decode_dims<T, true>(Q, K_cache, V_cache, O, L, batch_size, a, head_dim,
-                                    num_splits, stream);
+                                    num_splits, kAllocate, stream);
 }
+
+// ---------------------------------------------------------------------------------------------
+// Decode without allocation (cuflash_attention_decode_noalloc_f16): the split partials live in
+// `scratch`, a file-scope device array of kDecodeScratchBytes that every GPU the library runs on
+// holds until the process ends. Its device address is looked up once per device with that
+// device current (hipGetSymbolAddress: each GPU has its own copy at its own address); host code
+// only ever passes that address, never the array's name, to kernels. Calls on one GPU share the
+// array, so calls that overlap in time on one GPU (two streams, two host threads) race; calls
+// ordered on one stream do not. Nothing in it has to start at zero (see run_decode).
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first call per device).
+FlashAttentionError scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return FlashAttentionError::CUDA_ERROR;
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) return FlashAttentionError::CUDA_ERROR;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return FlashAttentionError::CUDA_ERROR;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FlashAttentionError::SUCCESS;
+}
+}  // namespace
+
+template <typename T>
+FlashAttentionError launch_decode_noalloc(const T* Q, const T* K, const T* V, T* O, float* L,
+                                          int batch_size, int num_heads, int kv_len,
+                                          int head_dim, float scale, int num_splits,
+                                          hipStream_t stream) {
+    void* ptr = nullptr;
+    FlashAttentionError err = scratch_address(&ptr);
+    if (err != FlashAttentionError::SUCCESS) return err;
+    const dev::DecodeArgs a = decode_args(num_heads, num_heads, kv_len, scale);
+    const FixedScratch fx{ptr, kDecodeScratchBytes};
+    return run_decode_dims<T, false>(Q, K, V, O, L, batch_size, a, head_dim, num_splits, fx,
+                                     stream);
+}
+
+template FlashAttentionError launch_decode_noalloc<__half>(const __half*, const __half*,
+                                                           const __half*, __half*, float*, int,
+                                                           int, int, int, float, int,
+                                                           hipStream_t);
 
 #define CUFLASH_DECODE_TYPE(T)                                                                  \
     template FlashAttentionError launch_decode<T>(const T*, const T*, const T*, T*, float*, int, \

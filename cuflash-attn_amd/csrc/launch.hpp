@@ -64,6 +64,18 @@ FlashAttentionError launch_decode_paged(const T* Q, const T* K_cache, const T* V
                                         int page_size, int max_pages_per_seq, int head_dim,
                                         float scale, int num_splits, hipStream_t stream);
 
+// Decode (as launch_decode) with the split partials in a fixed device array of
+// kDecodeScratchBytes per GPU instead of an allocated workspace: no allocation of any kind.
+// A call whose partials, B * H * splits * (head_dim + 2) * 4 bytes, exceed the array returns
+// OUT_OF_MEMORY before any launch. Calls that overlap in time on one GPU share the array and
+// race. Instantiated for __half.
+constexpr size_t kDecodeScratchBytes = size_t(32) << 20;
+template <typename T>
+FlashAttentionError launch_decode_noalloc(const T* Q, const T* K, const T* V, T* O, float* L,
+                                          int batch_size, int num_heads, int kv_len,
+                                          int head_dim, float scale, int num_splits,
+                                          hipStream_t stream);
+
 // Maps a HIP status after a launch or allocation to the library's error code.
 inline FlashAttentionError from_hip(hipError_t e) {
     if (e == hipSuccess) return FlashAttentionError::SUCCESS;

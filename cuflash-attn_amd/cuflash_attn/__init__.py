@@ -81,7 +81,7 @@ EXPORTED_SYMBOLS = (
     "cuflash_attention_forward_ext_f16", "cuflash_attention_forward_ext_bf16",
     "cuflash_attention_backward_ext_f32", "cuflash_attention_backward_ext_f16",
     "cuflash_attention_backward_ext_bf16", "cuflash_error_string", "cuflash_version",
-    "cuflash_profile_enable", "cuflash_profile_report",
+    "cuflash_profile_enable", "cuflash_profile_report", "cuflash_attention_decode_noalloc_f16",
 )
 
 
@@ -106,6 +106,8 @@ class CuFlashLibrary:
             fwd_ext.argtypes, fwd_ext.restype = _FWD_EXT_ARGS, ctypes.c_int
             bwd_ext = getattr(library, f"cuflash_attention_backward_ext_{sfx}")
             bwd_ext.argtypes, bwd_ext.restype = _BWD_EXT_ARGS, ctypes.c_int
+        noalloc = library.cuflash_attention_decode_noalloc_f16
+        noalloc.argtypes, noalloc.restype = _DEC_ARGS, ctypes.c_int
         library.cuflash_error_string.argtypes = [ctypes.c_int]
         library.cuflash_error_string.restype = ctypes.c_char_p
         library.cuflash_version.argtypes = []

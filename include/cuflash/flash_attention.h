@@ -261,6 +261,22 @@ CUFLASH_EXPORT int cuflash_attention_decode_bf16(const __hip_bfloat16* Q, const 
                                                  int kv_len, int head_dim, float scale,
                                                  int num_splits, hipStream_t stream);
 
+// Decode that allocates nothing. No counterpart in the reference: it is for callers that cannot
+// allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+// forbid hipMalloc). Same arguments, validation and results as cuflash_attention_decode_f16,
+// bitwise; the split partials, batch_size * num_heads * splits * (head_dim + 2) * 4 bytes, go to
+// a fixed 32 MiB device array that the library holds on every GPU it runs on until the process
+// ends, instead of a stream-ordered workspace. A call whose partials exceed 32 MiB returns
+// OUT_OF_MEMORY (5) before any device work (pass num_splits explicitly to bound them; config 4,
+// 16 x 32 heads at 64 splits, needs 16.3 MiB). Calls on one GPU share the array: calls that
+// overlap in time on one GPU (two streams, two host threads) race; calls ordered on one stream
+// do not.
+CUFLASH_EXPORT int cuflash_attention_decode_noalloc_f16(const __half* Q, const __half* K,
+                                                        const __half* V, __half* O, float* L,
+                                                        int batch_size, int num_heads, int kv_len,
+                                                        int head_dim, float scale, int num_splits,
+                                                        hipStream_t stream);
+
 // Grouped-query and paged decode ABI (additive; same arguments as the C++ functions above).
 CUFLASH_EXPORT int cuflash_attention_decode_gqa_f32(
     const float* Q, const float* K, const float* V, float* O, float* L, int batch_size, int num_heads,

@@ -35,7 +35,7 @@ def test_library_loads_from_reference_search_path(lib):
 
 def test_every_declared_symbol_is_exported(lib):
     declared = _declared_c_symbols()
-    assert len(declared) == 25, declared
+    assert len(declared) == 26, declared
     out = subprocess.run(["nm", "-D", "--defined-only", lib.path], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
