@@ -77,7 +77,8 @@ def committed_traffic(kernel_label):
 
 def pmc_workload(kind):
     """Short fixed workloads for rocprofv3 --pmc passes (no timing, no output line):
-    cfg3 = 2 x (forward + backward) of config 3; decode = 2 x config-4 decode (auto splits);
+    cfg3 = 2 x (forward + backward) of config 3; cfg1 / cfg2 = 2 x the forward of config 1 / 2;
+    cfg5 = 1 x (forward + backward) of config 5; decode = 2 x config-4 decode (auto splits);
     copy = one device-to-device copy of 1 GiB, the calibration kernel for FETCH_SIZE and
     WRITE_SIZE."""
     import torch
@@ -96,6 +97,16 @@ def pmc_workload(kind):
         for _ in range(2):
             o, lse = cuflash_attn.flash_attention_forward(*xs[:3], causal=True)
             cuflash_attn.flash_attention_backward(*xs[:3], o, lse, xs[3], causal=True)
+    elif kind in ("cfg1", "cfg2", "cfg5"):
+        name, sfx, B, H, N, D, causal, with_bwd, dist = next(
+            w for w in CONFIG_WORKLOADS if w[0] == kind)
+        dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[sfx]
+        std = 0.5 if dist == "N(0,0.5)" else 1.0
+        xs = [(torch.randn((B, H, N, D), device=dev) * std).to(dt) for _ in range(4)]
+        for _ in range(1 if with_bwd else 2):
+            o, lse = cuflash_attn.flash_attention_forward(*xs[:3], causal=causal)
+            if with_bwd:
+                cuflash_attn.flash_attention_backward(*xs[:3], o, lse, xs[3], causal=causal)
     elif kind == "decode":
         c = CFG4
         q = torch.randn((c["B"], c["H"], 1, c["D"]), device=dev).half()
@@ -120,7 +131,8 @@ def parse():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-ext", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
-    ap.add_argument("--pmc-workload", choices=("cfg3", "decode", "copy"), default=None,
+    ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "copy"),
+                    default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
     ap.add_argument("--cpu-seq", type=int, default=2048,
                     help="sequence length of the CPU baseline sample (default 2048)")

@@ -1254,10 +1254,9 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     const long long dthreads = rows * LPR;
     const long long dblocks = (dthreads + 255) / 256;
     if (dblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    int tok = profile_kernel<T, D>("backward_delta", stream);
-    hipLaunchKernelGGL((dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
+    int tok = profile_kernel<T, D>("backward_delta");
+    launch_kernel(tok, (dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, o, delta, rows);
-    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
@@ -1274,31 +1273,28 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     // the two bodies' LDS arrays add up).
     if constexpr (D <= 128) {
         if (qblocks + kblocks <= compute_units()) {
-            tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
-            hipLaunchKernelGGL((dev::dq_dkdv_kernel<T, D>),
+            tok = profile_kernel<T, D>("backward_dq_dkdv");
+            launch_kernel(tok, (dev::dq_dkdv_kernel<T, D>),
                                dim3(static_cast<unsigned>(qblocks + kblocks)), dim3(256), 0,
                                stream, q, k, v, L, go, delta, reinterpret_cast<E*>(dQ),
                                reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk,
                                coff, sh.group, nqb, nkb, static_cast<int>(kblocks), c, scale,
                                causal ? 1 : 0);
-            profile_end(tok, stream);
             return from_hip(hipGetLastError());
         }
     }
-    tok = profile_kernel<T, D>("backward_dq", stream);
-    hipLaunchKernelGGL((dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(qblocks)),
+    tok = profile_kernel<T, D>("backward_dq");
+    launch_kernel(tok, (dev::dq_kernel<T, D>), dim3(static_cast<unsigned>(qblocks)),
                        dim3(QCfg::kThreads), 0, stream, q, k, v, L, go, delta,
                        reinterpret_cast<E*>(dQ), sh.Nq, sh.Nk, coff, sh.group, nqb, c, scale,
                        causal ? 1 : 0);
-    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
-    tok = profile_kernel<T, D>("backward_dkdv", stream);
-    hipLaunchKernelGGL((dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(kblocks)),
+    tok = profile_kernel<T, D>("backward_dkdv");
+    launch_kernel(tok, (dev::dkdv_kernel<T, D>), dim3(static_cast<unsigned>(kblocks)),
                        dim3(KCfg::kThreads), 0, stream, q, k, v, L, go, delta,
                        reinterpret_cast<E*>(dK), reinterpret_cast<E*>(dV), sh.Nq, sh.Nk, coff,
                        sh.group, nkb, c, scale, causal ? 1 : 0);
-    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     return err;
 }
@@ -1339,11 +1335,10 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
     const uint16_t* v = reinterpret_cast<const uint16_t*>(V);
     const uint16_t* go = reinterpret_cast<const uint16_t*>(dO);
 
-    int tok = profile_kernel<T, D>("backward_delta", stream);
-    hipLaunchKernelGGL((dev::delta_ld_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
+    int tok = profile_kernel<T, D>("backward_delta");
+    launch_kernel(tok, (dev::delta_ld_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, sh.Nq, Npad,
                        rows_pad, queues);
-    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
 
@@ -1358,24 +1353,22 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
     // The resident workgroups (one or two per CU) take the qblocks + kblocks work items.
     const long long pool = std::min<long long>(
         qblocks + kblocks, static_cast<long long>(dev::bwd_fused_wgs_per_cu<D>()) * compute_units());
-    tok = profile_kernel<T, D>("backward_dq_dkdv", stream);
+    tok = profile_kernel<T, D>("backward_dq_dkdv");
     auto kernel = shares ? dev::bwd_fused_kernel<T, D, true> : dev::bwd_fused_kernel<T, D, false>;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
+    launch_kernel(tok, kernel, dim3(static_cast<unsigned>(pool)), dim3(256), 0, stream, q, k, v,
                        ld, go, reinterpret_cast<uint16_t*>(dQ), reinterpret_cast<uint16_t*>(dK),
                        reinterpret_cast<uint16_t*>(dV), sh.Nq, sh.Nk, sh.Nk - sh.Nq, sh.group,
                        Npad, nqb, nkb, sh.BH, c, scale, causal ? 1 : 0, queues, part);
-    profile_end(tok, stream);
     err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS || !shares) return err;
 
     const long long kv_elems = static_cast<long long>(sh.BH / sh.group) * sh.Nk * D;
     const long long rblocks = (kv_elems / 8 + 255) / 256;
-    tok = profile_kernel<T, D>("backward_dkdv_reduce", stream);
-    hipLaunchKernelGGL((dev::dkdv_reduce_kernel<T>), dim3(static_cast<unsigned>(rblocks)),
+    tok = profile_kernel<T, D>("backward_dkdv_reduce");
+    launch_kernel(tok, (dev::dkdv_reduce_kernel<T>), dim3(static_cast<unsigned>(rblocks)),
                        dim3(256), 0, stream, part, reinterpret_cast<uint16_t*>(dK),
                        reinterpret_cast<uint16_t*>(dV), kv_elems,
                        static_cast<long long>(sh.Nk) * D, sh.group);
-    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 

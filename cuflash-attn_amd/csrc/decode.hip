@@ -391,19 +391,17 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     float* part_acc = static_cast<float*>(base);
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(base) + acc_bytes);
 
-    int tok = profile_kernel<T, D>("decode_split", stream);
-    hipLaunchKernelGGL((dev::decode_split_kernel<T, D, G, PAGED>),
+    int tok = profile_kernel<T, D>("decode_split");
+    launch_kernel(tok, (dev::decode_split_kernel<T, D, G, PAGED>),
                        dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0, stream,
                        reinterpret_cast<const E*>(Q), reinterpret_cast<const E*>(K),
                        reinterpret_cast<const E*>(V), part_acc, part_ml, a);
-    profile_end(tok, stream);
     FlashAttentionError err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
-    tok = profile_kernel<T, D>("decode_combine", stream);
-    hipLaunchKernelGGL((dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(bhq)),
+    tok = profile_kernel<T, D>("decode_combine");
+    launch_kernel(tok, (dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(bhq)),
                        dim3(D), 0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L,
                        a.nsplit);
-    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 

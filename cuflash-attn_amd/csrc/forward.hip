@@ -1414,7 +1414,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int coff = sh.Nk - sh.Nq;
-    const int tok = profile_kernel<T, D>("forward", stream);
+    const int tok = profile_kernel<T, D>("forward");
     if constexpr (D == 64) {
         // Four-wave workgroups (two per CU, independent barriers, so one's prologue and
         // epilogue overlap the other's blocks) for non-causal launches and launches with
@@ -1425,7 +1425,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
             nqb = (sh.Nq + 32 * kWaves32 - 1) / (32 * kWaves32);
             blocks = static_cast<long long>(nqb) * sh.BH;
             if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-            hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves32, D>),
+            launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves32, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -1433,7 +1433,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                reinterpret_cast<uint16_t*>(O), L, sh.Nq, sh.Nk, coff, sh.group,
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
         } else {
-            hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves64, D>),
+            launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves64, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -1442,7 +1442,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
         }
     } else if constexpr (D == 32) {
-        hipLaunchKernelGGL((dev::fwd16_d64_kernel<T, kWaves32, D>),
+        launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves32, D>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
@@ -1450,7 +1450,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                            L, sh.Nq, sh.Nk, coff, sh.group, nqb, scale * dev::kLog2e,
                            causal ? 1 : 0);
     } else if constexpr (D == 256) {
-        hipLaunchKernelGGL((dev::fwd16_d256_kernel<T, kWaves256>),
+        launch_kernel(tok, (dev::fwd16_d256_kernel<T, kWaves256>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves256), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
@@ -1465,7 +1465,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
         if (blocks < compute_units()) {
             nqb = (sh.Nq + 32 * kWaves32 - 1) / (32 * kWaves32);
             blocks = static_cast<long long>(nqb) * sh.BH;
-            hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves32, D>),
+            launch_kernel(tok, (dev::fwd16_d128_kernel<T, kWaves32, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -1473,7 +1473,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                reinterpret_cast<uint16_t*>(O), L, sh.Nq, sh.Nk, coff, sh.group,
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
         } else {
-            hipLaunchKernelGGL((dev::fwd16_d128_kernel<T, kWaves128, D>),
+            launch_kernel(tok, (dev::fwd16_d128_kernel<T, kWaves128, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves128), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -1484,7 +1484,6 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     } else {
         static_assert(D == 32 || D == 64 || D == 96 || D == 128 || D == 256, "head_dim");
     }
-    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 
@@ -1496,7 +1495,7 @@ FlashAttentionError run_forward32(const float* Q, const float* K, const float* V
     const int nqb = (sh.Nq + Cfg::BM - 1) / Cfg::BM;
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    const int tok = profile_kernel<float, D>("forward", stream);
+    const int tok = profile_kernel<float, D>("forward");
     if constexpr (D <= 64) {
         // Fewer workgroups of 128 rows than two per CU: split each 32-row block's keys over
         // the four waves of a workgroup instead (fwd32_split_kernel).
@@ -1504,18 +1503,16 @@ FlashAttentionError run_forward32(const float* Q, const float* K, const float* V
             const int nqb32 = (sh.Nq + 31) / 32;
             const long long blocks32 = static_cast<long long>(nqb32) * sh.BH;
             if (blocks32 > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-            hipLaunchKernelGGL((dev::fwd32_split_kernel<D>), dim3(static_cast<unsigned>(blocks32)),
+            launch_kernel(tok, (dev::fwd32_split_kernel<D>), dim3(static_cast<unsigned>(blocks32)),
                                dim3(256), 0, stream, Q, K, V, O, L, sh.Nq, sh.Nk, sh.Nk - sh.Nq,
                                sh.group, nqb32, compute_units() / dev::kNumXcd,
                                scale * dev::kLog2e, causal ? 1 : 0);
-            profile_end(tok, stream);
             return from_hip(hipGetLastError());
         }
     }
-    hipLaunchKernelGGL((dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
+    launch_kernel(tok, (dev::fwd32_kernel<D>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::kThreads), 0, stream, Q, K, V, O, L, sh.Nq, sh.Nk,
                        sh.Nk - sh.Nq, sh.group, nqb, scale * dev::kLog2e, causal ? 1 : 0);
-    profile_end(tok, stream);
     return from_hip(hipGetLastError());
 }
 

@@ -18,13 +18,13 @@ namespace {
 
 struct Record {
     std::string label;
-    hipEvent_t start = nullptr;
-    hipEvent_t stop = nullptr;
+    ProfileEvents ev;
 };
 
 std::atomic<int> g_enabled{0};
 std::mutex g_mu;
 std::vector<Record> g_records;
+std::vector<ProfileEvents> g_free;  // created event pairs not in use
 
 }  // namespace
 
@@ -43,26 +43,44 @@ const char* dtype_tag<__hip_bfloat16>() {
 
 bool profiling_on() { return g_enabled.load(std::memory_order_relaxed) != 0; }
 
-int profile_begin(const char* label, hipStream_t stream) {
+int profile_begin(const char* label) {
     if (!g_enabled.load(std::memory_order_relaxed)) return -1;
     Record r;
     r.label = label;
-    if (hipEventCreate(&r.start) != hipSuccess) return -1;
-    if (hipEventCreate(&r.stop) != hipSuccess) {
-        (void)hipEventDestroy(r.start);
-        return -1;
-    }
-    (void)hipEventRecord(r.start, stream);
     std::lock_guard<std::mutex> lock(g_mu);
+    if (!g_free.empty()) {
+        r.ev = g_free.back();
+        g_free.pop_back();
+    } else {
+        if (hipEventCreate(&r.ev.start) != hipSuccess) return -1;
+        if (hipEventCreate(&r.ev.stop) != hipSuccess) {
+            (void)hipEventDestroy(r.ev.start);
+            return -1;
+        }
+    }
     g_records.push_back(r);
     return static_cast<int>(g_records.size()) - 1;
 }
 
-void profile_end(int token, hipStream_t stream) {
-    if (token < 0) return;
+ProfileEvents profile_events(int token) {
+    if (token < 0) return ProfileEvents{};
     std::lock_guard<std::mutex> lock(g_mu);
-    if (token < static_cast<int>(g_records.size()))
-        (void)hipEventRecord(g_records[token].stop, stream);
+    if (token >= static_cast<int>(g_records.size())) return ProfileEvents{};
+    return g_records[token].ev;
+}
+
+// Pre-creates event pairs so that a timed region's launches find them in the pool.
+void profile_reserve(int pairs) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    while (static_cast<int>(g_free.size()) < pairs) {
+        ProfileEvents ev;
+        if (hipEventCreate(&ev.start) != hipSuccess) return;
+        if (hipEventCreate(&ev.stop) != hipSuccess) {
+            (void)hipEventDestroy(ev.start);
+            return;
+        }
+        g_free.push_back(ev);
+    }
 }
 
 }  // namespace detail
@@ -71,6 +89,7 @@ void profile_end(int token, hipStream_t stream) {
 extern "C" {
 
 void cuflash_profile_enable(int enabled) {
+    if (enabled) cuflash::detail::profile_reserve(256);
     cuflash::detail::g_enabled.store(enabled ? 1 : 0, std::memory_order_relaxed);
 }
 
@@ -84,14 +103,16 @@ int cuflash_profile_report(char* buf, int buflen) {
     std::map<std::string, std::pair<long, double>> agg;
     for (Record& r : recs) {
         float ms = 0.0f;
-        if (hipEventSynchronize(r.stop) == hipSuccess &&
-            hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+        if (hipEventSynchronize(r.ev.stop) == hipSuccess &&
+            hipEventElapsedTime(&ms, r.ev.start, r.ev.stop) == hipSuccess) {
             auto& a = agg[r.label];
             a.first += 1;
             a.second += ms;
         }
-        (void)hipEventDestroy(r.start);
-        (void)hipEventDestroy(r.stop);
+    }
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        for (Record& r : recs) g_free.push_back(r.ev);
     }
     std::string out;
     char line[256];

@@ -2,13 +2,18 @@
 
 // Opt-in per-kernel timing with HIP events (measurement hook for benchmarks).
 //
-// When enabled through cuflash_profile_enable(1), every kernel launch of the library is
-// bracketed by two hipEventRecord calls on the launch stream; cuflash_profile_report() waits
-// for the recorded events and returns, per kernel label, the launch count and the summed
-// event-to-event time. Disabled (the default), profile_begin() is a single relaxed atomic load.
+// When enabled through cuflash_profile_enable(1), every kernel launch of the library is made with
+// hipExtLaunchKernelGGL and a start / stop event pair, which HIP fills with the dispatch's own
+// begin and end timestamps (the interval a kernel trace reports, with no queue gap before the
+// kernel counted). The pairs come from a pool created once, so the launch path creates nothing.
+// cuflash_profile_report() waits for the recorded events and returns, per kernel label, the
+// launch count and the summed kernel time. Disabled (the default), profile_kernel() is a single
+// relaxed atomic load and launch_kernel() launches without events.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdio>
 
 namespace cuflash {
@@ -16,20 +21,35 @@ namespace detail {
 
 bool profiling_on();
 
-// Returns a token for profile_end(), or -1 when profiling is off.
-int profile_begin(const char* label, hipStream_t stream);
-void profile_end(int token, hipStream_t stream);
+// Returns a token for launch_kernel(), or -1 when profiling is off.
+int profile_begin(const char* label);
+
+struct ProfileEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+// The event pair of a token (both null for -1).
+ProfileEvents profile_events(int token);
 
 template <typename T>
 const char* dtype_tag();
 
 // profile_begin with the label "<kernel>_<dtype>_d<head_dim>".
 template <typename T, int D>
-int profile_kernel(const char* kernel, hipStream_t stream) {
+int profile_kernel(const char* kernel) {
     if (!profiling_on()) return -1;
     char label[96];
     std::snprintf(label, sizeof(label), "%s_%s_d%d", kernel, dtype_tag<T>(), D);
-    return profile_begin(label, stream);
+    return profile_begin(label);
+}
+
+// Launches `kernel` on `stream`; with a profiling token, its events record the kernel's own
+// start and end.
+template <typename... Args, typename F>
+void launch_kernel(int token, F kernel, const dim3& grid, const dim3& block, uint32_t lds_bytes,
+                   hipStream_t stream, Args... args) {
+    const ProfileEvents ev = profile_events(token);
+    hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, ev.start, ev.stop, 0u, args...);
 }
 
 }  // namespace detail
