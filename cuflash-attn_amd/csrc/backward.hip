@@ -1245,7 +1245,7 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     const int BHkv = sh.BH / sh.group;
 
     const long long rows = static_cast<long long>(sh.BH) * sh.Nq;
-    StreamWorkspace ws(stream);
+    StreamWorkspace ws(stream, true);
     FlashAttentionError err = ws.alloc(static_cast<size_t>(rows) * sizeof(float));
     if (err != FlashAttentionError::SUCCESS) return err;
     float* delta = static_cast<float*>(ws.get());
@@ -1308,7 +1308,7 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
                                                hipStream_t stream) {
     const int Npad = (sh.Nq + 31) / 32 * 32;
     const long long rows_pad = static_cast<long long>(sh.BH) * Npad;
-    StreamWorkspace ws(stream);
+    StreamWorkspace ws(stream, true);
     // (L log2 e, D) rows, then the kNumXcd work-queue counters of bwd_fused_kernel
     const size_t ld_bytes = static_cast<size_t>(rows_pad) * sizeof(float2);
     FlashAttentionError err = ws.alloc(ld_bytes + dev::kNumXcd * sizeof(int));

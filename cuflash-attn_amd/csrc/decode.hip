@@ -377,7 +377,7 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
 
     const size_t acc_bytes = static_cast<size_t>(slots) * D * sizeof(float);
     const size_t ml_bytes = static_cast<size_t>(slots) * sizeof(float2);
-    StreamWorkspace ws(stream);
+    StreamWorkspace ws(stream, true);
     void* base = fixed.ptr;
     if (base != nullptr) {
         if (acc_bytes + ml_bytes > fixed.bytes) return FlashAttentionError::OUT_OF_MEMORY;

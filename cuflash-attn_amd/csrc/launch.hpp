@@ -4,6 +4,8 @@
 // kernels (forward.hip, backward.hip, decode.hip). Arguments have already been validated when a
 // launcher runs; launchers only check the HIP runtime.
 
+#include <mutex>
+
 #include "cuflash/flash_attention.h"
 
 namespace cuflash {
@@ -93,19 +95,43 @@ int compute_units();
 // be created (the workspaces then come from the device's current pool).
 hipMemPool_t workspace_pool();
 
-// Stream-ordered device workspace (hipMallocFromPoolAsync / hipFreeAsync on the caller's stream),
-// the counterpart of the reference's AsyncFloatBuffer (src/backward/flash_attention_backward_typed.cu
-// :374-394). Freed in stream order when the launcher returns, so the host never synchronizes and
-// concurrent calls on different streams never share memory.
+// A device buffer kept per (device, stream) for the launchers' small workspaces: the first
+// call on a stream allocates it stream-ordered from workspace_pool(), later calls reuse it, and a
+// call that needs more replaces it (the old one is freed stream-ordered, after every earlier use
+// on the stream). Reusing it saves each call the stream-ordered allocation and free, which leave
+// the GPU idle for about 6 us between the call's last kernel and the next work on the stream.
+// The returned lock holds the entry until the caller's kernels are enqueued, so that two host
+// threads on one stream cannot free a buffer the other is about to use; calls on different
+// streams never share one. Up to kStreamCacheBytes per (device, stream) stay allocated until the
+// process ends. hipStreamPerThread names a different stream in every host thread, so it is not
+// cached (stream_cached_buffer returns false).
+constexpr size_t kStreamCacheBytes = size_t(64) << 20;
+struct StreamCacheEntry;
+bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
+                          std::unique_lock<std::mutex>* lock, FlashAttentionError* err);
+
+// Stream-ordered device workspace, the counterpart of the reference's AsyncFloatBuffer
+// (src/backward/flash_attention_backward_typed.cu:374-394). Either the stream's cached buffer
+// (`cached`, for workspaces of at most kStreamCacheBytes; at most one cached workspace per call)
+// or a per-call hipMallocFromPoolAsync / hipFreeAsync on the caller's stream. Either way the host
+// never synchronizes and concurrent calls on different streams never share memory.
 class StreamWorkspace {
 public:
-    explicit StreamWorkspace(hipStream_t stream) : stream_(stream) {}
+    explicit StreamWorkspace(hipStream_t stream, bool cached = false)
+        : stream_(stream), cached_(cached) {}
     StreamWorkspace(const StreamWorkspace&) = delete;
     StreamWorkspace& operator=(const StreamWorkspace&) = delete;
     ~StreamWorkspace() {
-        if (ptr_) (void)hipFreeAsync(ptr_, stream_);
+        if (ptr_ && owned_) (void)hipFreeAsync(ptr_, stream_);
     }
     FlashAttentionError alloc(size_t bytes) {
+        if (cached_ && bytes <= kStreamCacheBytes) {
+            FlashAttentionError err = FlashAttentionError::SUCCESS;
+            if (stream_cached_buffer(stream_, bytes, &ptr_, &lock_, &err)) {
+                owned_ = false;
+                return err;
+            }
+        }
         hipMemPool_t pool = workspace_pool();
         hipError_t e = pool ? hipMallocFromPoolAsync(&ptr_, bytes, pool, stream_)
                             : hipMallocAsync(&ptr_, bytes, stream_);
@@ -115,13 +141,17 @@ public:
             return e == hipErrorOutOfMemory ? FlashAttentionError::OUT_OF_MEMORY
                                             : FlashAttentionError::CUDA_ERROR;
         }
+        owned_ = true;
         return FlashAttentionError::SUCCESS;
     }
     void* get() const { return ptr_; }
 
 private:
     hipStream_t stream_;
+    bool cached_;
+    bool owned_ = false;
     void* ptr_ = nullptr;
+    std::unique_lock<std::mutex> lock_;  // held while the cached buffer is in use by this call
 };
 
 }  // namespace detail

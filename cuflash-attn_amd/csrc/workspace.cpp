@@ -5,9 +5,15 @@
 // device whose release threshold is kKeepBytes keeps the few MiB the launchers usually use (the
 // backward's row statistics, the decode partials) cached, gives larger workspaces (grouped-query
 // dK/dV shares) back at synchronization, and leaves the application's pools alone.
+// stream_cached_buffer keeps one buffer per (device, stream) from that pool for the small
+// per-call workspaces (see launch.hpp).
 
+#include <algorithm>
 #include <cstdint>
+#include <map>
+#include <memory>
 #include <mutex>
+#include <utility>
 
 #include "launch.hpp"
 
@@ -50,6 +56,58 @@ hipMemPool_t workspace_pool() {
         }
     }
     return g_pools[dev];
+}
+
+struct StreamCacheEntry {
+    std::mutex use;  // held by the call that is enqueuing work with the buffer
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+namespace {
+std::mutex g_cache_mutex;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamCacheEntry>> g_cache;
+}  // namespace
+
+bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
+                          std::unique_lock<std::mutex>* lock, FlashAttentionError* err) {
+    if (stream == hipStreamPerThread) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    StreamCacheEntry* e = nullptr;
+    {
+        std::lock_guard<std::mutex> guard(g_cache_mutex);
+        std::unique_ptr<StreamCacheEntry>& slot = g_cache[{dev, stream}];
+        if (!slot) slot.reset(new StreamCacheEntry());
+        e = slot.get();
+    }
+    std::unique_lock<std::mutex> use(e->use);
+    if (e->bytes < bytes) {
+        // Grow to at least twice the old size (in whole MiB, at most kStreamCacheBytes).
+        size_t want = std::max(bytes, std::min(2 * e->bytes, kStreamCacheBytes));
+        want = std::min(kStreamCacheBytes, (want + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1));
+        void* p = nullptr;
+        hipMemPool_t pool = workspace_pool();
+        const hipError_t r = pool ? hipMallocFromPoolAsync(&p, want, pool, stream)
+                                  : hipMallocAsync(&p, want, stream);
+        if (r != hipSuccess) {
+            (void)hipGetLastError();
+            *err = r == hipErrorOutOfMemory ? FlashAttentionError::OUT_OF_MEMORY
+                                            : FlashAttentionError::CUDA_ERROR;
+            *out = nullptr;
+            return true;
+        }
+        if (e->ptr) (void)hipFreeAsync(e->ptr, stream);  // after every earlier use on the stream
+        e->ptr = p;
+        e->bytes = want;
+    }
+    *out = e->ptr;
+    *err = FlashAttentionError::SUCCESS;
+    *lock = std::move(use);
+    return true;
 }
 
 int compute_units() {

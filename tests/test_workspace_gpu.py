@@ -59,3 +59,99 @@ def test_decode_workspace_larger_than_the_device_returns_out_of_memory(torch_gpu
     assert max_abs(synth.to_numpy(od), o_ref) <= 2e-2
     assert max_abs(synth.to_numpy(ld), l_ref) <= 2e-2
     assert np.isfinite(synth.to_numpy(ld)).all()
+
+
+def _bwd_case(torch, n, seed, h=4):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    q, k, v, do = (torch.randn((1, h, n, 128), generator=g, device="cuda").to(torch.bfloat16)
+                   for _ in range(4))
+    return q, k, v, do
+
+
+@pytest.mark.gpu
+def test_cached_workspace_grows_and_is_reused_in_stream_order(torch_gpu):
+    """The backward's and decode's workspaces are one cached buffer per stream: calls of
+    growing and shrinking size on one stream, back to back with no synchronization, give the
+    results of the same calls made one at a time with a synchronization after each."""
+    torch = torch_gpu
+    sizes = [64, 2048, 300, 4096, 1000]
+    cases = [_bwd_case(torch, n, 30 + i) for i, n in enumerate(sizes)]
+    ref = []
+    for q, k, v, do in cases:
+        o, lse = cuflash_attn.flash_attention_forward(q, k, v, causal=True)
+        g = cuflash_attn.flash_attention_backward(q, k, v, o, lse, do, causal=True)
+        torch.cuda.synchronize()
+        ref.append((o, lse) + tuple(g))
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        got = []
+        for q, k, v, do in cases:
+            o, lse = cuflash_attn.flash_attention_forward(q, k, v, causal=True)
+            got.append((o, lse) + tuple(cuflash_attn.flash_attention_backward(
+                q, k, v, o, lse, do, causal=True)))
+        # decode partials share the stream's buffer: small, large, small
+        dec = []
+        for bh, kv_len, splits in ((2, 512, 4), (64, 32768, 64), (4, 100, 2)):
+            g = torch.Generator(device="cuda")
+            g.manual_seed(kv_len)
+            qd = torch.randn((1, bh, 1, 128), generator=g, device="cuda").half()
+            kd = torch.randn((1, bh, kv_len, 128), generator=g, device="cuda").half()
+            vd = torch.randn((1, bh, kv_len, 128), generator=g, device="cuda").half()
+            dec.append(((qd, kd, vd, splits),
+                        cuflash_attn.flash_attention_decode(qd, kd, vd, num_splits=splits)))
+    torch.cuda.synchronize()
+    for r, g in zip(ref, got):
+        for a, b in zip(r, g):
+            assert torch.equal(a, b)
+    for (args, (o, lse)) in dec:
+        o2, l2 = cuflash_attn.flash_attention_decode(*args[:3], num_splits=args[3])
+        torch.cuda.synchronize()
+        assert torch.equal(o, o2) and torch.equal(lse, l2)
+
+
+@pytest.mark.gpu
+def test_concurrent_host_threads_on_one_stream(torch_gpu):
+    """Host threads that call the backward on the same stream at the same time, with different
+    workspace sizes (so the stream's cached buffer grows while other calls use it), get the
+    results of serial calls. ctypes releases the interpreter lock during each call."""
+    import threading
+
+    torch = torch_gpu
+    sizes = [128, 4096, 512, 2048, 256, 3000]
+    cases = [_bwd_case(torch, n, 60 + i, h=8) for i, n in enumerate(sizes)]
+    fwd = []
+    for q, k, v, do in cases:
+        fwd.append(cuflash_attn.flash_attention_forward(q, k, v, causal=True))
+    torch.cuda.synchronize()
+    ref = []
+    for (q, k, v, do), (o, lse) in zip(cases, fwd):
+        ref.append(cuflash_attn.flash_attention_backward(q, k, v, o, lse, do, causal=True))
+        torch.cuda.synchronize()
+    lib = cuflash_attn.load_library()
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    outs = [[torch.empty_like(c[0]) for _ in range(3)] for c in cases]
+    errors = []
+
+    def worker(i):
+        q, k, v, do = cases[i]
+        o, lse = fwd[i]
+        fn = lib.fn("backward", "bf16")
+        for _ in range(5):
+            st = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                    do.data_ptr(), outs[i][0].data_ptr(), outs[i][1].data_ptr(),
+                    outs[i][2].data_ptr(), 1, 8, q.shape[2], 128, 128 ** -0.5, True, sp)
+            if st != 0:
+                errors.append((i, st))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for r, g in zip(ref, outs):
+        for a, b in zip(r, g):
+            assert torch.equal(a, b)
