@@ -216,8 +216,13 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 
     // One block with an explicit instruction order (the scheduling fences keep it), so that
     // each MFMA is followed by a few VALU ops that do not depend on it:
-    //   phase A: the 16 MFMAs of the next block's scores (K tile kt) into s_next, each with the
-    //            exponential of one score of the current tile 0 (P groups 0 and 1);
+    //   phase A: the 16 MFMAs of the next block's scores (K tile kt) into s_next; after the
+    //            first kDelay of them the online-softmax update with the current block's max
+    //            mx_cur (formed in the previous phase B; its dependent chain of cross-lane max,
+    //            compare, exp2 and ballot then overlaps MFMAs in flight instead of idling both
+    //            waves of a SIMD before the barrier: config 3 1.3-3% faster, bitwise equal), then
+    //            with each MFMA the exponential of one score of the current tile 0 (P groups 0
+    //            and 1);
     //   phase B: the 16 MFMAs of O^T += V^T P^T (V tile vt), the first eight with the
     //            exponentials of two scores of tile 1 (P groups 2 and 3, first used by MFMA 8),
     //            each with two terms of the row sum and the max of two scores of s_next.
@@ -233,15 +238,12 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
                     const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
                     unsigned char* kl_dst, bool vl_do, int vl_key0,
-                    unsigned char* vl_dst) -> float {
+                    unsigned char* vl_dst, float mx_cur) -> float {
         constexpr int kAhead = 3;
         constexpr int kMma = 4 * NDT;  // MFMAs per phase (16 at head_dim 128, 12 at 96)
+        constexpr int kDelay = 3;      // phase-A MFMAs before the max update
         static_assert(kAhead <= kMma, "operands read ahead within the chain");
-        // VALU work is dealt over the MFMAs of a phase by index ranges [n i / kMma,
-        // n (i + 1) / kMma): at head_dim 128 one tile-0 exponential per phase-A MFMA, two tile-1
-        // exponentials per MFMA of phase B's first half, one row-sum pair and one max step per
-        // phase-B MFMA.
-        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        float m_use = 0.0f;
         frag p[4];
         frag fk[kMma];
         frag fv[kMma];
@@ -262,10 +264,23 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                 if (i == (j + 1) * h / kParts - 1 && kl_do) load_part(Kh, kl_key0, kl_dst, j);
                 if (i == h + (j + 1) * h / kParts - 1 && vl_do) load_part(Vh, vl_key0, vl_dst, j);
             }
+            if (i == kDelay - 1) {
+                // Online-softmax update with this block's max (formed in the previous phase B),
+                // here where its latency overlaps the score MFMAs in flight.
+                float alpha;
+                if (update_max(mx_cur, alpha)) {
 #pragma unroll
-            for (int e = 16 * i / kMma; e < 16 * (i + 1) / kMma; ++e) {
-                exp_one(s, 0, e, m_use);
-                if ((e & 7) == 7) p[e >> 3] = pack_p(s, 0, e >> 3);
+                    for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+                }
+                m_use = (m == -INFINITY) ? 0.0f : m;
+            }
+            if (i >= kDelay) {
+                constexpr int kN = kMma - kDelay;
+#pragma unroll
+                for (int e = 16 * (i - kDelay) / kN; e < 16 * (i - kDelay + 1) / kN; ++e) {
+                    exp_one(s, 0, e, m_use);
+                    if ((e & 7) == 7) p[e >> 3] = pack_p(s, 0, e >> 3);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -306,27 +321,24 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
     // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
     // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
-    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and their row max (for the
-    // last block they come from a stale buffer and the max is replaced by -inf, which leaves
-    // (m, l) unchanged). The loop is unrolled by two so that every buffer is a distinct LDS
-    // object.
+    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and
+    // their row max, which the next iteration applies (for the last block they come from a
+    // stale buffer and the max is never used). The loop is unrolled by two so that every buffer
+    // is a distinct LDS object.
     load_tile(Kh, 0, Kb0);
     load_tile(Vh, 0, Vb0);
     if (nkb > 1) load_tile(Kh, BN, Kb1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     f32x16 sa[2], sb[2];
-    float alpha;
     scores(Kb0, sa);
     if (needs_mask(0)) mask_scores(sa, 0);
-    {
-        float mx = -INFINITY;
+    // Raw row max of the block whose scores are in the current set (step() applies it).
+    float mx = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
-        }
-        update_max(mx, alpha);  // O is still zero: nothing to rescale
+        for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
     }
     // Key blocks this wave computes: with a causal mask its rows see keys up to q0 + 31 + coff,
     // and up to three of the workgroup's last four blocks lie entirely past them (the keys of
@@ -340,12 +352,8 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
         // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
-                        j + 1 < nkb, (j + 1) * BN, Vb1);
-        if (update_max(j + 1 < nkb_w ? mx : -INFINITY, alpha)) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
-        }
+        mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                  j + 1 < nkb, (j + 1) * BN, Vb1, mx);
         if (j + 1 >= nkb_w) {
             ++j;
             break;
@@ -354,11 +362,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
-                  j + 2 < nkb, (j + 2) * BN, Vb0);
-        if (update_max(j + 2 < nkb_w ? mx : -INFINITY, alpha)) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
-        }
+                  j + 2 < nkb, (j + 2) * BN, Vb0, mx);
     }
     // Load-only iterations j = nkb_w .. nkb - 1 (the same buffers as the compute iterations).
     for (j = nkb_w; j < nkb; ++j) {
@@ -704,6 +708,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
                       float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
                       float c, int causal) {
     static_assert(D == 64 || D == 32, "rows of at most 128 bytes");
+    // Online-softmax update inside the next step (as in fwd16_d128_kernel) except for the
+    // four-wave workgroups at head_dim 64 (non-causal launches), where phase A's exponentials then
+    // crowd the VALU: config 2 measured 6% slower with it, eight-wave causal 3% faster.
+    constexpr bool kLateMax = !(NW == 4 && D == 64);
     constexpr int KS = D / 16;   // k-steps of a score MFMA chain
     constexpr int NDT = D / 32;  // 32-column tiles of O
     constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
@@ -868,27 +876,33 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // One block with an explicit instruction order (the scheduling fences keep it), as in
     // fwd16_d128_kernel with half the MFMAs per phase (the softmax work per key is the same, so
     // every MFMA carries twice the VALU work):
-    //   phase A: the 8 MFMAs of the next block's scores into s_next, each with the exponentials
-    //            of two scores of the current tile 0 (P groups 0 and 1); the wave's K load part
-    //            after MFMA 1, its V load part after MFMA 5;
+    //   phase A: the 8 MFMAs of the next block's scores into s_next; after the first
+    //            kDelay = 2 the online-softmax update with the current block's max (as in
+    //            fwd16_d128_kernel), then the exponentials of the current tile 0 spread over the
+    //            remaining 6 (P groups 0 and 1); the wave's K load part after MFMA 1, its V load
+    //            part after MFMA 5;
     //   phase B: the 8 MFMAs of O^T += V^T P^T; MFMAs 0-3 carry the exponentials of tile 1
     //            (P groups 2 and 3, first used by MFMAs 4 and 6), every MFMA four terms of the
     //            fp32 row sum and the max of four scores of s_next.
-    // At head_dim 32 each phase has 4 MFMAs: phase A four exponentials per MFMA, the V load part
-    // after MFMA 3; phase B eight exponentials in each of MFMAs 0-1 and eight row-sum / max terms
+    // At head_dim 32 each phase has 4 MFMAs: phase A the update after MFMA 0, then 16
+    // exponentials over MFMAs 1-3, the V load part after MFMA 3; phase B eight exponentials in each of MFMAs 0-1 and eight row-sum / max terms
     // per MFMA.
     // Returns this lane's raw row max of s_next.
     auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
                     const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
                     unsigned char* kl_dst, bool vl_do, int vl_key0,
-                    unsigned char* vl_dst) -> float {
+                    unsigned char* vl_dst, float mx_cur) -> float {
         constexpr int kAhead = 3;
         constexpr int kMma = 4 * NDT;  // MFMAs per phase (8 at head_dim 64, 4 at 32)
         static_assert(kAhead <= kMma, "operands read ahead within the chain");
-        constexpr int kExpA = 16 / kMma;        // tile-0 exponentials per phase-A MFMA
+        // Phase-A MFMAs before the max update (kLateMax), and those that carry the tile-0
+        // exponentials; without kLateMax the update runs after the step and the exponentials
+        // start with MFMA 0.
+        constexpr int kDelay = kLateMax ? kMma / 4 : 0;
+        constexpr int kN = kMma - kDelay;
         constexpr int kExpB = 16 / (kMma / 2);  // tile-1 exponentials per early phase-B MFMA
         constexpr int kQuads = 8 / kMma;        // 4-term row sum / max groups per phase-B MFMA
-        const float m_use = (m == -INFINITY) ? 0.0f : m;
+        float m_use = kLateMax ? 0.0f : ((m == -INFINITY) ? 0.0f : m);
         frag p[4];
         frag fk[kMma];
         frag fv[kMma];
@@ -909,10 +923,22 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 #pragma unroll
                 for (int part = 0; part < kParts; ++part) load_part(Vh, vl_key0, vl_dst, part);
             }
+            if (kLateMax && i == kDelay - 1) {
+                // Online-softmax update with this block's max (see fwd16_d128_kernel).
+                float alpha;
+                if (update_max(mx_cur, alpha)) {
 #pragma unroll
-            for (int e = 0; e < kExpA; ++e) exp_one(s, 0, kExpA * i + e, m_use);
-            if ((i + 1) * kExpA % 8 == 0)
-                p[(i + 1) * kExpA / 8 - 1] = pack_p(s, 0, (i + 1) * kExpA / 8 - 1);
+                    for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+                }
+                m_use = (m == -INFINITY) ? 0.0f : m;
+            }
+            if (i >= kDelay) {
+#pragma unroll
+                for (int e = 16 * (i - kDelay) / kN; e < 16 * (i - kDelay + 1) / kN; ++e) {
+                    exp_one(s, 0, e, m_use);
+                    if ((e & 7) == 7) p[e >> 3] = pack_p(s, 0, e >> 3);
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         if (needs_mask(key0_next)) mask_scores(s_next, key0_next);
@@ -952,55 +978,80 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Block j: K_j in Kb[j & 1], V_j in Vb[j & 1]. At the top of iteration j the loads issued
     // one iteration earlier (K_{j+1}, V_j) are waited for and a barrier makes them visible and
     // retires every read of K_j and V_{j-1}; then K_{j+2} and V_{j+1} are issued into those
-    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and their row max (for the
-    // last block they come from a stale buffer and the max is replaced by -inf, which leaves
-    // (m, l) unchanged). The loop is unrolled by two so that every buffer is a distinct LDS
-    // object.
+    // buffers during the score MFMAs. Each iteration also forms the scores of block j+1 and
+    // their row max, which the next iteration applies (for the last block they come from a
+    // stale buffer and the max is never used). The loop is unrolled by two so that every buffer
+    // is a distinct LDS object.
     load_tile(Kh, 0, Kb0);
     load_tile(Vh, 0, Vb0);
     if (nkb > 1) load_tile(Kh, BN, Kb1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     f32x16 sa[2], sb[2];
-    float alpha;
     scores(Kb0, sa);
     if (needs_mask(0)) mask_scores(sa, 0);
-    {
+    // Key blocks this wave computes (see fwd16_d128_kernel): after the last one that is not
+    // entirely past its rows' causal limit the wave runs load-only iterations. Not at head_dim 32
+    // (four-wave workgroups of 128 rows: measured 2.7% slower with it).
+    const int nkb_w = (causal && D == 64) ? min(nkb, (q0 + 32 + coff + BN - 1) / BN) : nkb;
+    int j = 0;
+    if constexpr (kLateMax) {
+        // Raw row max of the block whose scores are in the current set (step() applies it).
         float mx = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
         }
-        update_max(mx, alpha);  // O is still zero: nothing to rescale
-    }
-    // Key blocks this wave computes (see fwd16_d128_kernel): after the last one that is not
-    // entirely past its rows' causal limit the wave runs load-only iterations. Not at head_dim 32
-    // (four-wave workgroups of 128 rows: measured 2.7% slower with it).
-    const int nkb_w = (causal && D == 64) ? min(nkb, (q0 + 32 + coff + BN - 1) / BN) : nkb;
-    int j = 0;
-    for (; j < nkb_w; j += 2) {
-        // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
-                        j + 1 < nkb, (j + 1) * BN, Vb1);
-        if (update_max(j + 1 < nkb_w ? mx : -INFINITY, alpha)) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+        for (; j < nkb_w; j += 2) {
+            // ---- even block j: scores in sa, K_j in Kb0, V_j in Vb0 ----
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                      j + 1 < nkb, (j + 1) * BN, Vb1, mx);
+            if (j + 1 >= nkb_w) {
+                ++j;
+                break;
+            }
+            // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
+                      j + 2 < nkb, (j + 2) * BN, Vb0, mx);
         }
-        if (j + 1 >= nkb_w) {
-            ++j;
-            break;
-        }
-        // ---- odd block j + 1: scores in sb, K_{j+1} in Kb1, V_{j+1} in Vb1 ----
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
-                  j + 2 < nkb, (j + 2) * BN, Vb0);
-        if (update_max(j + 2 < nkb_w ? mx : -INFINITY, alpha)) {
+    } else {
+        // The next block's max is applied after each step.
+        float alpha;
+        {
+            float mx = -INFINITY;
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
+            }
+            update_max(mx, alpha);  // O is still zero: nothing to rescale
+        }
+        for (; j < nkb_w; j += 2) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
+                            j + 1 < nkb, (j + 1) * BN, Vb1, 0.0f);
+            if (update_max(j + 1 < nkb_w ? mx : -INFINITY, alpha)) {
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+            }
+            if (j + 1 >= nkb_w) {
+                ++j;
+                break;
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
+                      j + 2 < nkb, (j + 2) * BN, Vb0, 0.0f);
+            if (update_max(j + 2 < nkb_w ? mx : -INFINITY, alpha)) {
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+            }
         }
     }
     for (j = nkb_w; j < nkb; ++j) {
