@@ -375,8 +375,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert((NW == 8 || NW == 4) && 2 * staged_rows_bytes<D>() <= TILE,
-                  "two waves' O rows per K/V buffer");
+    static_assert(2 * staged_rows_bytes<D>() <= TILE, "two waves' O rows per K/V buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     store_rows_staged<T, D>(o, 1.0f / l,
@@ -692,26 +691,21 @@ __global__ void __launch_bounds__(64 * NW, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// fp16 / bf16 kernel for head_dim 64 and 32
+// fp16 / bf16 kernel for head_dim 64, causal launches
 // ------------------------------------------------------------------------------------------
-// fwd16_d128_kernel's data path and pipeline at head_dim 64 (config 2's shape): 64-key blocks
-// in LDS-DMA double buffers, one workgroup of NW waves per CU, the next block's scores formed
+// fwd16_d128_kernel's data path and pipeline at head_dim 64: 64-key blocks in LDS-DMA double
+// buffers, one workgroup of eight waves (256 query rows) per CU, the next block's scores formed
 // while the current block's softmax runs. A 64-element row is 128 bytes, so one load
 // instruction (64 lanes x 16 bytes) fills a group of 8 rows; the group layout is given at the
-// operand offsets below. At head_dim 32 a row takes the first half of its 128-byte slot (the
-// same layout, read with two k-steps per score chain and one 32-column O tile), and every
-// phase has half the MFMAs, each carrying twice the VALU work.
+// operand offsets below (fwd16_d64_seq_kernel uses the same one; at head_dim 32 a row takes the
+// first half of its 128-byte slot).
 template <typename T, int NW, int D>
 __global__ void __launch_bounds__(64 * NW, 8 / NW)
     fwd16_d64_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                       float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
                       float c, int causal) {
-    static_assert(D == 64 || D == 32, "rows of at most 128 bytes");
-    // Online-softmax update inside the next step (as in fwd16_d128_kernel) except for the
-    // four-wave workgroups at head_dim 64 (non-causal launches), where phase A's exponentials then
-    // crowd the VALU: config 2 measured 6% slower with it, eight-wave causal 3% faster.
-    constexpr bool kLateMax = !(NW == 4 && D == 64);
+    static_assert(NW == 8 && D == 64, "eight waves at head_dim 64 (fwd16_d64_seq_kernel otherwise)");
     constexpr int KS = D / 16;   // k-steps of a score MFMA chain
     constexpr int NDT = D / 32;  // 32-column tiles of O
     constexpr int BM = 32 * NW;  // query rows per workgroup (NW waves of 32 rows)
@@ -884,25 +878,20 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     //   phase B: the 8 MFMAs of O^T += V^T P^T; MFMAs 0-3 carry the exponentials of tile 1
     //            (P groups 2 and 3, first used by MFMAs 4 and 6), every MFMA four terms of the
     //            fp32 row sum and the max of four scores of s_next.
-    // At head_dim 32 each phase has 4 MFMAs: phase A the update after MFMA 0, then 16
-    // exponentials over MFMAs 1-3, the V load part after MFMA 3; phase B eight exponentials in each of MFMAs 0-1 and eight row-sum / max terms
-    // per MFMA.
     // Returns this lane's raw row max of s_next.
     auto step = [&](f32x16 (&s)[2], const unsigned char* kt, f32x16 (&s_next)[2],
                     const unsigned char* vt, int key0_next, bool kl_do, int kl_key0,
                     unsigned char* kl_dst, bool vl_do, int vl_key0,
                     unsigned char* vl_dst, float mx_cur) -> float {
         constexpr int kAhead = 3;
-        constexpr int kMma = 4 * NDT;  // MFMAs per phase (8 at head_dim 64, 4 at 32)
+        constexpr int kMma = 4 * NDT;  // MFMAs per phase
         static_assert(kAhead <= kMma, "operands read ahead within the chain");
-        // Phase-A MFMAs before the max update (kLateMax), and those that carry the tile-0
-        // exponentials; without kLateMax the update runs after the step and the exponentials
-        // start with MFMA 0.
-        constexpr int kDelay = kLateMax ? kMma / 4 : 0;
+        // Phase-A MFMAs before the max update, and those that carry the tile-0 exponentials.
+        constexpr int kDelay = kMma / 4;
         constexpr int kN = kMma - kDelay;
         constexpr int kExpB = 16 / (kMma / 2);  // tile-1 exponentials per early phase-B MFMA
         constexpr int kQuads = 8 / kMma;        // 4-term row sum / max groups per phase-B MFMA
-        float m_use = kLateMax ? 0.0f : ((m == -INFINITY) ? 0.0f : m);
+        float m_use = 0.0f;
         frag p[4];
         frag fk[kMma];
         frag fv[kMma];
@@ -923,7 +912,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 #pragma unroll
                 for (int part = 0; part < kParts; ++part) load_part(Vh, vl_key0, vl_dst, part);
             }
-            if (kLateMax && i == kDelay - 1) {
+            if (i == kDelay - 1) {
                 // Online-softmax update with this block's max (see fwd16_d128_kernel).
                 float alpha;
                 if (update_max(mx_cur, alpha)) {
@@ -991,11 +980,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     scores(Kb0, sa);
     if (needs_mask(0)) mask_scores(sa, 0);
     // Key blocks this wave computes (see fwd16_d128_kernel): after the last one that is not
-    // entirely past its rows' causal limit the wave runs load-only iterations. Not at head_dim 32
-    // (four-wave workgroups of 128 rows: measured 2.7% slower with it).
-    const int nkb_w = (causal && D == 64) ? min(nkb, (q0 + 32 + coff + BN - 1) / BN) : nkb;
+    // entirely past its rows' causal limit the wave runs load-only iterations.
+    const int nkb_w = causal ? min(nkb, (q0 + 32 + coff + BN - 1) / BN) : nkb;
     int j = 0;
-    if constexpr (kLateMax) {
+    {
         // Raw row max of the block whose scores are in the current set (step() applies it).
         float mx = -INFINITY;
 #pragma unroll
@@ -1019,40 +1007,6 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
             mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
                       j + 2 < nkb, (j + 2) * BN, Vb0, mx);
         }
-    } else {
-        // The next block's max is applied after each step.
-        float alpha;
-        {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, sa[t][r]);
-            }
-            update_max(mx, alpha);  // O is still zero: nothing to rescale
-        }
-        for (; j < nkb_w; j += 2) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            float mx = step(sa, Kb1, sb, Vb0, (j + 1) * BN, j + 2 < nkb, (j + 2) * BN, Kb0,
-                            j + 1 < nkb, (j + 1) * BN, Vb1, 0.0f);
-            if (update_max(j + 1 < nkb_w ? mx : -INFINITY, alpha)) {
-#pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
-            }
-            if (j + 1 >= nkb_w) {
-                ++j;
-                break;
-            }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            mx = step(sb, Kb0, sa, Vb1, (j + 2) * BN, j + 3 < nkb, (j + 3) * BN, Kb1,
-                      j + 2 < nkb, (j + 2) * BN, Vb0, 0.0f);
-            if (update_max(j + 2 < nkb_w ? mx : -INFINITY, alpha)) {
-#pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
-            }
-        }
     }
     for (j = nkb_w; j < nkb; ++j) {
         __builtin_amdgcn_s_waitcnt(0);
@@ -1064,13 +1018,221 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     // Epilogue: O = O / l, L = m + log(l) (natural log), stored with RNE. O goes through the K/V
     // buffers (two waves' rows per buffer), free once every wave is past its last block.
     l = pair_sum(l);
-    static_assert((NW == 8 || NW == 4) && 2 * staged_rows_bytes<D>() <= TILE,
-                  "two waves' O rows per K/V buffer");
+    static_assert(2 * staged_rows_bytes<D>() <= TILE, "two waves' O rows per K/V buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     store_rows_staged<T, D>(o, 1.0f / l,
                             (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
                                 (wave & 1) * staged_rows_bytes<D>(),
+                            O + head, q0, Nq);
+    if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
+}
+
+// ------------------------------------------------------------------------------------------
+// fp16 / bf16 kernel for head_dim 64 and 32, four workgroups per CU
+// ------------------------------------------------------------------------------------------
+// fwd16_d64_kernel's tiles, operand layouts and arithmetic without its cross-block pipeline:
+// each wave forms a block's scores, applies the block's max, forms the exponentials and runs the
+// P V MFMAs in sequence, with one score set. That fits 128 registers, so four workgroups of four
+// waves (16 waves, 4 x 36 KB of tiles) share a CU and the SIMD interleaves four waves' phases
+// instead of relying on one wave's instruction order. For non-causal launches at head_dim 64
+// (config 2: 1024 workgroups, all resident at once instead of in two and a third rounds) and
+// every launch at head_dim 32. Same products, sums and rounding in the same order as
+// fwd16_d64_kernel<T, 4, D>, so the results are bitwise equal.
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 4)
+    fwd16_d64_seq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                         const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
+                         float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
+                         float c, int causal) {
+    static_assert(D == 64 || D == 32, "rows of at most 128 bytes");
+    constexpr int NW = 4;
+    constexpr int KS = D / 16;   // k-steps of a score MFMA chain
+    constexpr int NDT = D / 32;  // 32-column tiles of O
+    constexpr int BM = 32 * NW;  // query rows per workgroup
+    constexpr int BN = 64;
+    constexpr int kParts = 8 / NW;         // load instructions per wave per 64-row tile
+    constexpr int GRP = 1152;              // bytes per 8-row group (fwd16_d64_kernel's layout)
+    constexpr int TILE = (BN / 8) * GRP;   // bytes per 64-row tile
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
+
+    int bh, rank;
+    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const size_t head = static_cast<size_t>(bh) * Nq * D;             // Q, O
+    const size_t kv_head = static_cast<size_t>(bh / group) * Nk * D;  // K, V
+    const uint16_t* Kh = K + kv_head;
+    const uint16_t* Vh = V + kv_head;
+    const int q0 = qb * BM + wave * 32;  // first query row of this wave
+    const int q = q0 + l32;              // query row owned by this lane
+
+    frag qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < Nq) v = ld16(Q + head + static_cast<size_t>(q) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+    const int kv_end = causal ? min(Nk, (qb + 1) * BM + coff) : Nk;
+    const int nkb = (kv_end + BN - 1) / BN;
+
+    // Tile loads, operand offsets and masking exactly as in fwd16_d64_kernel.
+    const int ld_row = (lane & 7) ^ (4 * ((lane >> 4) & 1));
+    const int ld_col = ((lane >> 3) % (D / 8)) * 8;
+    const unsigned ld_voff = static_cast<unsigned>(((8 * wave + ld_row) * D + ld_col) * 2);
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+#pragma unroll
+        for (int i = 0; i < kParts; ++i) {
+            if (key0 + BN <= Nk) {
+                lds_dma16_async_s(src + static_cast<size_t>(key0 + 8 * NW * i) * D, ld_voff,
+                                  dst + (wave + NW * i) * GRP);
+            } else {
+                const int grp = wave + NW * i;
+                const int row = min(key0 + 8 * grp + ld_row, Nk - 1);
+                lds_dma16_async(src + static_cast<size_t>(row) * D + ld_col, dst + grp * GRP);
+            }
+        }
+    };
+    const int k_off_even = (l32 >> 3) * GRP + g2 * 128 + (l32 & 7) * 16;
+    const int k_off_odd = (l32 >> 3) * GRP + g2 * 128 + ((l32 & 7) ^ 4) * 16;
+    const int kq = lane & 15;
+    const int gl = (lane >> 4) & 1;
+    const int v_off = (2 * gl + ((kq & 3) >> 1)) * 128 + (g2 ^ gl) * 64 + (kq >> 2) * 16 +
+                      (kq & 1) * 8;
+    auto k_frag = [&](const unsigned char* kt, int i) {  // K rows of tile i / KS, k-step i % KS
+        const int t = i / KS, ks = i % KS;
+        return as_frag<T>(ld16(kt + ((ks & 1) ? k_off_odd : k_off_even) + 4 * t * GRP + ks * 256));
+    };
+    auto v_frag = [&](const unsigned char* vt, int i) {  // V^T, key group i / NDT, d tile i % NDT
+        const unsigned char* a0 = vt + v_off + 2 * (i / NDT) * GRP + (i % NDT) * 512;
+        return tr_frag_at<T>(a0, a0 + GRP);
+    };
+
+    f32x16 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;  // running max of s * cs (log2 units)
+    float l = 0.0f;       // this lane's share of the running row sum
+    const float cs = fmaxf(c, kFltMin);
+
+    // One block: scores, the block's max, exponentials and row sum, then O^T += V^T P^T.
+    auto block = [&](const unsigned char* kt, const unsigned char* vt, int key0) {
+        constexpr int kAhead = 3;
+        constexpr int kMma = 4 * NDT;  // MFMAs per chain (score tiles x k-steps = key groups x d tiles)
+        static_assert(2 * KS == kMma && kAhead <= kMma, "chain lengths");
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+        {
+            frag fk[kMma];
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) fk[k] = k_frag(kt, k);
+#pragma unroll
+            for (int i = 0; i < kMma; ++i) {
+                if (i + kAhead < kMma) fk[i + kAhead] = k_frag(kt, i + kAhead);
+                s[i / KS] = Elem<T>::mma(fk[i], qf[i % KS], s[i / KS]);
+            }
+        }
+        if (key0 + BN > Nk || (causal && key0 + BN - 1 > q0 + coff)) {
+            const int lim = min(Nk, causal ? q + 1 + coff : Nk) - key0 - 4 * g2;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int off = 32 * t + 8 * (r >> 2) + (r & 3);
+                    s[t][r] = off < lim ? s[t][r] : -INFINITY;
+                }
+            }
+        }
+        // Online-softmax update (lazy rescale, as in fwd16_d64_kernel).
+        {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, s[t][r]);
+            }
+            const float m_new = fmaxf(m, pair_max(mx) * cs);
+            const bool grow = m_new > m + kLazyRescale;
+            const float a_raw = fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new);
+            const float alpha = grow ? a_raw : 1.0f;
+            m = grow ? m_new : m;
+            l *= alpha;
+            if (__ballot(grow) != 0) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+            }
+        }
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[t][r] = fast_exp2(fmaf(s[t][r], cs, -m_use));
+        }
+        frag p[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int t = g >> 1, h = g & 1;
+            p[g] = pack_frag<T>(s[t][8 * h + 0], s[t][8 * h + 1], s[t][8 * h + 2], s[t][8 * h + 3],
+                                s[t][8 * h + 4], s[t][8 * h + 5], s[t][8 * h + 6], s[t][8 * h + 7]);
+        }
+        // Row sum of the fp32 exponentials, four terms per group, in fwd16_d64_kernel's order.
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int t = i >> 2;
+            const int r = 4 * (i & 3);
+            sum += (s[t][r] + s[t][r + 1]) + (s[t][r + 2] + s[t][r + 3]);
+        }
+        l += sum;
+        {
+            frag fv[kMma];
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) fv[k] = v_frag(vt, k);
+#pragma unroll
+            for (int i = 0; i < kMma; ++i) {
+                if (i + kAhead < kMma) fv[i + kAhead] = v_frag(vt, i + kAhead);
+                o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
+            }
+        }
+    };
+
+    // Block j in Kb[j & 1], Vb[j & 1]; the loads of block j + 1 are issued right after the
+    // barrier that retires every read of block j - 1. Unrolled by two so that every buffer is a
+    // distinct LDS object.
+    load_tile(Kh, 0, Kb0);
+    load_tile(Vh, 0, Vb0);
+    for (int j = 0; j < nkb; j += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 1 < nkb) {
+            load_tile(Kh, (j + 1) * BN, Kb1);
+            load_tile(Vh, (j + 1) * BN, Vb1);
+        }
+        block(Kb0, Vb0, j * BN);
+        if (j + 1 >= nkb) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 2 < nkb) {
+            load_tile(Kh, (j + 2) * BN, Kb0);
+            load_tile(Vh, (j + 2) * BN, Vb0);
+        }
+        block(Kb1, Vb1, (j + 1) * BN);
+    }
+
+    // Epilogue as in fwd16_d64_kernel: O = O / l, L = m + log(l), O rows staged through LDS.
+    l = pair_sum(l);
+    static_assert(2 * staged_rows_bytes<D>() <= TILE, "two waves' O rows per K buffer");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    store_rows_staged<T, D>(o, 1.0f / l, (wave < 2 ? Kb0 : Kb1) + (wave & 1) * staged_rows_bytes<D>(),
                             O + head, q0, Nq);
     if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
 }
@@ -1467,16 +1629,17 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     const int coff = sh.Nk - sh.Nq;
     const int tok = profile_kernel<T, D>("forward");
     if constexpr (D == 64) {
-        // Four-wave workgroups (two per CU, independent barriers, so one's prologue and
-        // epilogue overlap the other's blocks) for non-causal launches and launches with
-        // fewer eight-wave workgroups than CUs; eight-wave ones for causal launches, whose
-        // K/V tiles then serve twice the rows (config 2: 104.6 -> 99.0 us with four waves;
-        // causal B=2 H=16 N=4096: 87.6 us with eight, 90.6 with four).
+        // Four-wave workgroups of the sequential kernel (four per CU, independent barriers)
+        // for non-causal launches and launches with fewer eight-wave workgroups than CUs;
+        // the pipelined eight-wave kernel for causal launches, whose K/V tiles then serve
+        // twice the rows (config 2: 93 -> 86 us with the sequential kernel against the
+        // pipelined one at four waves; causal B=2 H=16 N=4096 bf16: 86.9 us with eight waves,
+        // 97.7 with the sequential kernel).
         if (!causal || blocks < compute_units()) {
             nqb = (sh.Nq + 32 * kWaves32 - 1) / (32 * kWaves32);
             blocks = static_cast<long long>(nqb) * sh.BH;
             if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-            launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves32, D>),
+            launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -1493,7 +1656,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
         }
     } else if constexpr (D == 32) {
-        launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves32, D>),
+        launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
