@@ -483,18 +483,21 @@ def main():
         nbytes = decode_bytes(Bd, Hd, LKV, Dd)
 
         def time_calls(fn):
-            """ms per call over args.steps calls with no event hook (the hook's events between
-            the split and combine launches cost time of their own), then the per-kernel
-            report of a second pass with the hook on."""
+            """ms per call: the median of 5 regions of args.steps calls with no event hook (the
+            hook's events between the split and combine launches cost time of their own), then
+            the per-kernel report of a further pass with the hook on."""
             for _ in range(3):
                 fn()
             torch.cuda.synchronize()
-            t0.record(stream)
-            for _ in range(args.steps):
-                fn()
-            t1.record(stream)
-            torch.cuda.synchronize()
-            ms = t0.elapsed_time(t1) / args.steps
+            regions = []
+            for _ in range(5):
+                t0.record(stream)
+                for _ in range(args.steps):
+                    fn()
+                t1.record(stream)
+                torch.cuda.synchronize()
+                regions.append(t0.elapsed_time(t1) / args.steps)
+            ms = sorted(regions)[len(regions) // 2]
             lib.profile_enable(True)
             for _ in range(args.steps):
                 fn()
