@@ -1132,10 +1132,13 @@ __device__ __forceinline__ int xcc_id() {
 }
 
 // Resident workgroups per CU: two, except at head_dim 256, whose dK/dV accumulators and K/V
-// operands need the registers of a whole SIMD lane.
+// operands need the registers of a whole SIMD lane, and at head_dim 32, whose items fit 128
+// registers, so four share a CU (causal B=2 H=16 N=4096: 217.5 -> 206.8 us; config 2's shape at
+// head_dim 32: 219.7 -> 196.4 us). Three at head_dim 64 would need 168 registers; the compiler
+// then spills and the launch is no faster.
 template <int D>
 constexpr int bwd_fused_wgs_per_cu() {
-    return D >= 256 ? 1 : 2;
+    return D >= 256 ? 1 : D == 32 ? 4 : 2;
 }
 
 template <typename T, int D, bool kShares>
