@@ -3,7 +3,8 @@
 The fp16/bf16 forward at head_dim 128 and 96 runs 256-row (eight-wave) workgroups whenever
 B * H * ceil(Nq / 256) is at least the number of compute units (256 on an MI355X), and four-wave
 128-row ones below that; at head_dim 64 the eight-wave workgroups run for causal launches of
-that size. The small shapes of test_ext_gpu.py and test_parity_gpu.py all take the four-wave
+that size, and every other head_dim-64 launch and every head_dim-32 launch runs the sequential
+four-wave kernel (four workgroups per CU), checked here at the same wide shapes. The small shapes of test_ext_gpu.py and test_parity_gpu.py all take the four-wave
 path, so these tests use B = 1, H = 32 and Nq in {2000, 2049}, which reach the eight-wave kernel
 with the code that only runs there: a partial last key tile (Nk not a multiple of 64), query rows
 past Nq in the last workgroup, the causal offset Nk - Nq > 0 with its per-wave stop, and
@@ -87,11 +88,18 @@ def test_eight_wave_forward_d64_causal(torch_gpu, hkv):
     _check_forward(torch_gpu, "bfloat16", 64, hkv, (True,), seed0=64 + hkv)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("d,causal_list", [(64, (False,)), (32, (True, False))])
+@pytest.mark.parametrize("hkv", [32, 8])
+def test_sequential_forward_d64_d32_wide(torch_gpu, d, causal_list, hkv):
+    _check_forward(torch_gpu, "float16", d, hkv, causal_list, seed0=700 + d + hkv)
+
+
 BWD_CASES = [(2000, 2000, True), (2049, 8195, True), (2049, 8195, False)]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("d", [128, 96, 64])
+@pytest.mark.parametrize("d", [128, 96, 64, 32])
 @pytest.mark.parametrize("hkv", [32, 8])
 def test_backward_ext_at_wide_launch_sizes(torch_gpu, d, hkv):
     torch = torch_gpu
