@@ -8,8 +8,9 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
   value = (F_fwd + F_bwd) / step time with the reference's FLOP model
   (benchmarks/bench_flash_attention.cu:34-44, causal x0.5 at :457-460):
   F_fwd = 4 B H N^2 D / 2, F_bwd = 2.5 F_fwd.
-* The K timed steps run as five consecutive regions (events between them, one synchronized
-  bracket around all of them); ms_per_step is the median region's time per step.
+* The K timed steps (default 100) run as five consecutive regions of K/5 steps (events between
+  them, one synchronized bracket around all of them); ms_per_step is the median region's time
+  per step.
 * Decode (config 4: fp16, B=16 H=32, 1 query, 32768 keys, D=128) is timed for 16/32/64 splits
   (the headline: the best of these, config 4's range) and the library's automatic choice
   (reported beside it); GB/s counts K and V read once plus Q read, O and L written.
@@ -121,7 +122,7 @@ def pmc_workload(kind):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ramp-ms", type=float, default=1000.0,
                     help="untimed steps for at least this long before the warmup steps, so that "
