@@ -560,7 +560,7 @@ def main():
                      Bd, Hd, Hkv, LKV, Dd, Dd ** -0.5, 0, sp)
             if st != 0:
                 raise RuntimeError(f"decode_gqa status {st}")
-        ext = {"gqa": time_ext(run_gqa, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}")}
+        dext = {"gqa": time_ext(run_gqa, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}")}
 
         npages = Bd * LKV // page
         kp = kg.reshape(Bd, Hkv, LKV // page, page, Dd).permute(0, 2, 3, 1, 4).reshape(
@@ -581,9 +581,9 @@ def main():
                        Dd ** -0.5, 0, sp)
             if st != 0:
                 raise RuntimeError(f"decode_paged status {st}")
-        ext["paged"] = time_ext(run_paged, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}, "
+        dext["paged"] = time_ext(run_paged, f"fp16 B={Bd} H={Hd} Hkv={Hkv} Lkv={LKV} D={Dd}, "
                                            f"{page}-key pages in shuffled order")
-        decode["extensions"] = ext
+        decode["extensions"] = dext
         del kp, vp, table, lens, perm
 
     # ---------------- CPU baseline (bounded sample) ----------------
