@@ -1029,24 +1029,25 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
 }
 
 // ------------------------------------------------------------------------------------------
-// fp16 / bf16 kernel for head_dim 64 and 32, four workgroups per CU
+// fp16 / bf16 kernel for head_dim 64 and 32, four waves per SIMD
 // ------------------------------------------------------------------------------------------
 // fwd16_d64_kernel's tiles, operand layouts and arithmetic without its cross-block pipeline:
 // each wave forms a block's scores, applies the block's max, forms the exponentials and runs the
-// P V MFMAs in sequence, with one score set. That fits 128 registers, so four workgroups of four
-// waves (16 waves, 4 x 36 KB of tiles) share a CU and the SIMD interleaves four waves' phases
-// instead of relying on one wave's instruction order. For non-causal launches at head_dim 64
-// (config 2: 1024 workgroups, all resident at once instead of in two and a third rounds) and
-// every launch at head_dim 32. Same products, sums and rounding in the same order as
-// fwd16_d64_kernel<T, 4, D>, so the results are bitwise equal.
-template <typename T, int D>
-__global__ void __launch_bounds__(256, 4)
+// P V MFMAs in sequence, with one score set. That fits 128 registers, so 16 waves share a CU
+// (four workgroups of four waves, or two of eight, each with 36 KB of tiles) and the SIMD
+// interleaves four waves' phases instead of relying on one wave's instruction order. Eight-wave
+// workgroups (256 rows) halve the tile loads per MFMA. Used for head_dim 64 launches except
+// causal ones with fewer than 8192 keys (there the pipelined kernel's per-wave causal stop saves
+// more) and for every launch at head_dim 32. Same products, sums and rounding in the same order
+// as fwd16_d64_kernel, so the results are bitwise equal.
+template <typename T, int D, int NW>
+__global__ void __launch_bounds__(64 * NW, 16 / NW)
     fwd16_d64_seq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                          const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                          float* __restrict__ L, int Nq, int Nk, int coff, int group, int nqb,
                          float c, int causal) {
     static_assert(D == 64 || D == 32, "rows of at most 128 bytes");
-    constexpr int NW = 4;
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
     constexpr int KS = D / 16;   // k-steps of a score MFMA chain
     constexpr int NDT = D / 32;  // 32-column tiles of O
     constexpr int BM = 32 * NW;  // query rows per workgroup
@@ -1232,7 +1233,9 @@ __global__ void __launch_bounds__(256, 4)
     static_assert(2 * staged_rows_bytes<D>() <= TILE, "two waves' O rows per K buffer");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    store_rows_staged<T, D>(o, 1.0f / l, (wave < 2 ? Kb0 : Kb1) + (wave & 1) * staged_rows_bytes<D>(),
+    store_rows_staged<T, D>(o, 1.0f / l,
+                            (wave < 2 ? Kb0 : wave < 4 ? Kb1 : wave < 6 ? Vb0 : Vb1) +
+                                (wave & 1) * staged_rows_bytes<D>(),
                             O + head, q0, Nq);
     if (g2 == 0 && q < Nq) L[static_cast<size_t>(bh) * Nq + q] = (m + fast_log2(l)) * kLn2;
 }
@@ -1629,24 +1632,22 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     const int coff = sh.Nk - sh.Nq;
     const int tok = profile_kernel<T, D>("forward");
     if constexpr (D == 64) {
-        // Four-wave workgroups of the sequential kernel (four per CU, independent barriers)
-        // for non-causal launches and launches with fewer eight-wave workgroups than CUs;
-        // the pipelined eight-wave kernel for causal launches, whose K/V tiles then serve
-        // twice the rows (config 2: 93 -> 86 us with the sequential kernel against the
-        // pipelined one at four waves; causal B=2 H=16 N=4096 bf16: 86.9 us with eight waves,
-        // 97.7 with the sequential kernel).
-        if (!causal || blocks < compute_units()) {
-            nqb = (sh.Nq + 32 * kWaves32 - 1) / (32 * kWaves32);
-            blocks = static_cast<long long>(nqb) * sh.BH;
-            if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-            launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D>),
-                               dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0,
+        // Launches with at least as many 256-row blocks as CUs: eight-wave workgroups of the
+        // sequential kernel (two per CU), except causal ones with fewer than 8192 keys, which
+        // take the pipelined kernel and its per-wave causal stop. Smaller launches: four-wave
+        // workgroups of the sequential kernel (twice the workgroups, four per CU). Measured
+        // (us): config 2 93 (pipelined, four waves) -> 86 (sequential, four) -> 85 (sequential,
+        // eight); causal bf16 B=2 H=16 N=4096: 86-89 pipelined, 97-100 sequential; causal
+        // B=1 H=32 N=8192: 332-343 pipelined, 302-313 sequential.
+        if (blocks >= compute_units() && (!causal || sh.Nk >= 8192)) {
+            launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D, kWaves64>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
                                reinterpret_cast<const uint16_t*>(V),
                                reinterpret_cast<uint16_t*>(O), L, sh.Nq, sh.Nk, coff, sh.group,
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
-        } else {
+        } else if (blocks >= compute_units()) {
             launch_kernel(tok, (dev::fwd16_d64_kernel<T, kWaves64, D>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves64), 0,
                                stream, reinterpret_cast<const uint16_t*>(Q),
@@ -1654,9 +1655,20 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
                                reinterpret_cast<const uint16_t*>(V),
                                reinterpret_cast<uint16_t*>(O), L, sh.Nq, sh.Nk, coff, sh.group,
                                nqb, scale * dev::kLog2e, causal ? 1 : 0);
+        } else {
+            nqb = (sh.Nq + 32 * kWaves32 - 1) / (32 * kWaves32);
+            blocks = static_cast<long long>(nqb) * sh.BH;
+            if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
+            launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D, kWaves32>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0,
+                               stream, reinterpret_cast<const uint16_t*>(Q),
+                               reinterpret_cast<const uint16_t*>(K),
+                               reinterpret_cast<const uint16_t*>(V),
+                               reinterpret_cast<uint16_t*>(O), L, sh.Nq, sh.Nk, coff, sh.group,
+                               nqb, scale * dev::kLog2e, causal ? 1 : 0);
         }
     } else if constexpr (D == 32) {
-        launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D>),
+        launch_kernel(tok, (dev::fwd16_d64_seq_kernel<T, D, kWaves32>),
                            dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves32), 0, stream,
                            reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
