@@ -691,7 +691,8 @@ __global__ void __launch_bounds__(64 * NW, 1)
 }
 
 // ------------------------------------------------------------------------------------------
-// fp16 / bf16 kernel for head_dim 64, causal launches
+// fp16 / bf16 kernel for head_dim 64: causal launches of at least as many 256-row blocks as CUs
+// with fewer than 8192 keys
 // ------------------------------------------------------------------------------------------
 // fwd16_d128_kernel's data path and pipeline at head_dim 64: 64-key blocks in LDS-DMA double
 // buffers, one workgroup of eight waves (256 query rows) per CU, the next block's scores formed
