@@ -1,0 +1,54 @@
+"""Tensors past 2^31 elements on the headline path (bf16, head_dim 128, causal forward and
+backward through the reference entry points).
+
+Q, K, V, O, dO, dQ, dK and dV each hold 2 x 65568 x 128 x 128 = 2^31 + 2^20 elements (about
+4.3 GB apiece, 35 GB in all), so every head from (1, 65504) on starts past element 2^31 and a
+32-bit product anywhere in an offset (head, row, tile or L / (L, D) index, in the forward, the
+delta pass or the fused backward) would read or write the wrong head. The inputs come from
+torch's GPU generator; the heads on both sides of the boundary and the last head are copied back
+and compared with the fp64 oracle on every row, to the north-star tolerance (2e-2 max-abs).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import cuflash_attn
+import oracle
+from conftest import max_abs
+
+TOL16 = 2e-2
+
+
+@pytest.mark.gpu
+def test_bf16_causal_fwd_bwd_past_2_31_elements(torch_gpu):
+    torch = torch_gpu
+    B, H, N, D = 2, 65568, 128, 128
+    assert B * H * N * D > 2 ** 31 and (B * H - 64) * N * D == 2 ** 31
+    scale = D ** -0.5
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    q, k, v, do = (torch.randn((B, H, N, D), device=dev, dtype=torch.bfloat16, generator=gen)
+                   for _ in range(4))
+    o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=scale, causal=True)
+    dq, dk, dv = cuflash_attn.flash_attention_backward(q, k, v, o, lse, do, scale=scale,
+                                                       causal=True)
+    torch.cuda.synchronize()
+    rows = np.arange(N)
+    # (0, 0): the first head; (1, 65503) ends at element 2^31; (1, 65504) starts there;
+    # (1, 65567): the last head.
+    for b, h in ((0, 0), (1, 65503), (1, 65504), (1, H - 1)):
+        host = [t[b:b + 1, h:h + 1].float().cpu().numpy().astype(np.float64)
+                for t in (q, k, v, do)]
+        got = [t[b:b + 1, h:h + 1].float().cpu().numpy() for t in (o, lse, dq, dk, dv)]
+        o_ref, l_ref = oracle.forward(host[0], host[1], host[2], scale, True)
+        assert max_abs(got[0], o_ref) <= TOL16, f"O {(b, h)}"
+        assert max_abs(got[1], l_ref) <= TOL16, f"L {(b, h)}"
+        rq, rk, rv = oracle.backward_rows(*host, scale, True, rows, rows)
+        assert max_abs(got[2], rq) <= TOL16, f"dQ {(b, h)}"
+        assert max_abs(got[3], rk) <= TOL16, f"dK {(b, h)}"
+        assert max_abs(got[4], rv) <= TOL16, f"dV {(b, h)}"
+    del q, k, v, do, o, lse, dq, dk, dv
+    torch.cuda.empty_cache()  # 35 GB back to the device for the tests that follow
