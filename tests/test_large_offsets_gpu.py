@@ -1,5 +1,5 @@
-"""Tensors past 2^31 elements on the headline path (bf16, head_dim 128, causal forward and
-backward through the reference entry points).
+"""Tensors past 2^31 elements: the headline path (bf16, head_dim 128, causal forward and
+backward through the reference entry points) and the split-KV decode.
 
 Q, K, V, O, dO, dQ, dK and dV each hold 2 x 65568 x 128 x 128 = 2^31 + 2^20 elements (about
 4.3 GB apiece, 35 GB in all), so every head from (1, 65504) on starts past element 2^31 and a
@@ -52,3 +52,30 @@ def test_bf16_causal_fwd_bwd_past_2_31_elements(torch_gpu):
         assert max_abs(got[4], rv) <= TOL16, f"dV {(b, h)}"
     del q, k, v, do, o, lse, dq, dk, dv
     torch.cuda.empty_cache()  # 35 GB back to the device for the tests that follow
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("splits", [16, 0])
+def test_fp16_decode_past_2_31_elements(torch_gpu, splits):
+    """Config 4's decode with one more batch row: K and V hold 17 x 32 x 32768 x 128 = 2^31 +
+    2^27 elements each, so batch row 16 starts at element 2^31 (config 4 itself ends exactly
+    there). Heads on both sides of the boundary and the last head against the oracle."""
+    torch = torch_gpu
+    B, H, LKV, D = 17, 32, 32768, 128
+    assert (B - 1) * H * LKV * D == 2 ** 31
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(32)
+    q = torch.randn((B, H, 1, D), device=dev, dtype=torch.float16, generator=gen)
+    k = torch.randn((B, H, LKV, D), device=dev, dtype=torch.float16, generator=gen)
+    v = torch.randn((B, H, LKV, D), device=dev, dtype=torch.float16, generator=gen)
+    o, lse = cuflash_attn.flash_attention_decode(q, k, v, scale=D ** -0.5, num_splits=splits)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (15, 31), (16, 0), (16, 31)):
+        qh, kh, vh = (t[b:b + 1, h:h + 1].float().cpu().numpy().astype(np.float64)
+                      for t in (q, k, v))
+        o_ref, l_ref = oracle.forward(qh, kh, vh, D ** -0.5, False)
+        assert max_abs(o[b:b + 1, h:h + 1].float().cpu().numpy(), o_ref) <= TOL16, f"O {(b, h)}"
+        assert max_abs(lse[b:b + 1, h:h + 1].float().cpu().numpy(), l_ref) <= TOL16, f"L {(b, h)}"
+    del q, k, v, o, lse
+    torch.cuda.empty_cache()
