@@ -126,18 +126,7 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 __device__ __forceinline__ void st16_nt(void* p, u32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
-__device__ __forceinline__ u32x2 ld8(const void* p) {
-    return *reinterpret_cast<const u32x2*>(p);
-}
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
-
-// Low / high 16-bit halves of two dwords packed into one dword.
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
-    return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-    return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
 
 // ---------------------------------------------------------------------------------------------
 // Row-tile store through LDS. A wave holds 32 rows of a [rows, D] 16-bit output as accumulator
@@ -305,12 +294,7 @@ __device__ __forceinline__ typename Elem<T>::frag tr_frag_at(const unsigned char
 // bytes at its own global address to lds_base + 16 * i (verified on gfx950). lds_base must be
 // wave-uniform; the load is tracked by vmcnt like any other global load.
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void lds_dma16(const void* src, unsigned char* lds_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_base), 16,
-                                     0, 0);
-}
-
-// The same loads issued from inline assembly. The compiler then does not know that they write
+// The loads are issued from inline assembly. The compiler then does not know that they write
 // LDS and adds no waits for them, so the kernel must order every LDS access itself
 // (s_waitcnt vmcnt(0) and a barrier before the data is read, and before a buffer is reused).
 // This lets a kernel rotate buffers with run-time offsets, where the compiler would otherwise
