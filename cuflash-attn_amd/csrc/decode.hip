@@ -17,6 +17,7 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "profile.hpp"
+#include "softmax.hpp"
 
 namespace cuflash {
 namespace dev {
@@ -296,6 +297,219 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// LDS-DMA loads (common.hpp's lds_dma16_async / lds_dma16_async_s) with the non-temporal hint:
+// a decode reads each key / value row once, so the stream should not displace cached lines.
+__device__ __forceinline__ void lds_dma16_nt(const void* src, unsigned char* lds_base) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
+                                               unsigned char* lds_base) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :
+                 : "v"(voff), "s"(sbase),
+                   "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
+                 : "memory");
+}
+
+// ------------------------------------------------------------------------------------------
+// Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 128, contiguous K / V)
+// ------------------------------------------------------------------------------------------
+// With several query heads per key/value head, decode_split_kernel is bound by its vector ALU
+// (per key and query head: a 16-lane dot product, its reduction and an 8-wide accumulator
+// update). Here the G <= 32 query heads of one key/value head are the columns of the forward
+// kernels' transposed 32 x 32 tiles: S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16, one
+// lane per query head (the lanes of columns past G carry zero queries and store nothing), so the
+// vector work per key is the softmax of one score per head. One wave per (batch, key/value head,
+// split) streams the split's keys in 32-key blocks through LDS-DMA double buffers in the
+// forward's 4-row group layout (K row reads and V transpose reads conflict-free), the next
+// block's loads in flight while the current one is consumed; the split's chunk is a multiple
+// of 32 keys, so only the last block of a sequence is partial (its rows past the end are
+// clamped to the last key and masked). Output: decode_split_kernel's partial (m, l, acc) per
+// (query head, split), with m lazily rescaled as in the forward (acc and l always refer to the
+// stored m, so the combine is exact).
+// The LDS (34 KB per workgroup) allows four workgroups, one wave per SIMD; at that register
+// budget the compiler keeps the score and O accumulators in AGPRs (16 v_accvgpr_read per
+// block feed the softmax, O is read back only for a rescale and at the end).
+template <typename T>
+__global__ void __launch_bounds__(64)
+    decode_mma_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                      const uint16_t* __restrict__ V, float* __restrict__ part_acc,
+                      float2* __restrict__ part_ml, DecodeArgs a) {
+    constexpr int D = 128;
+    constexpr int KS = D / 16;   // k-steps of the score MFMA chain
+    constexpr int NDT = D / 32;  // 32-column tiles of O^T
+    constexpr int BN = 32;       // keys per block
+    constexpr int GRP = 1088;    // bytes per 4-row group
+    constexpr int TILE = (BN / 4) * GRP;
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[TILE];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
+
+    // blockIdx.x = (b * Hkv + hk) * nsplit + split.
+    const int hpk = a.H / a.Hkv;
+    int rest = blockIdx.x;
+    const int split = rest % a.nsplit;
+    rest /= a.nsplit;
+    const int hk = rest % a.Hkv;
+    const int b = rest / a.Hkv;
+    const int h0 = hk * hpk;
+    const int lane = threadIdx.x;
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const int kbeg = split * a.chunk;
+    const int kend = min(a.kv_len, kbeg + a.chunk);
+    const int nblk = kend > kbeg ? (kend - kbeg + BN - 1) / BN : 0;
+    const uint16_t* Kh = K + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
+    const uint16_t* Vh = V + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
+
+    // Q^T: lane l32 holds query head h0 + l32 (zeros past the group), dims 16 ks + 8 g2 .. + 8.
+    frag qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (l32 < hpk) v = ld16(Q + (static_cast<size_t>(b) * a.H + h0 + l32) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    // Tile loads: group g (rows key0 + 4 g .. + 3) by one instruction, lane i: row i % 4,
+    // 16-byte chunk i / 4. Whole tiles use a scalar base; the last one clamps rows to kend - 1.
+    const int ld_row = lane & 3;
+    const int ld_col = (lane >> 2) * 8;
+    const unsigned ld_voff = static_cast<unsigned>((ld_row * D + ld_col) * 2);
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+        if (key0 + BN <= kend) {
+#pragma unroll
+            for (int g = 0; g < BN / 4; ++g)
+                lds_dma16_nt_s(src + static_cast<size_t>(key0 + 4 * g) * D, ld_voff, dst + g * GRP);
+        } else {
+#pragma unroll
+            for (int g = 0; g < BN / 4; ++g) {
+                const int row = min(key0 + 4 * g + ld_row, kend - 1);
+                lds_dma16_nt(src + static_cast<size_t>(row) * D + ld_col, dst + g * GRP);
+            }
+        }
+    };
+    // Operand offsets of the forward's layout: K rows (lane l32 = key, chunk 2 ks + g2) and the
+    // V transpose reads (key group i / NDT, dim tile i % NDT).
+    const int k_off = (l32 >> 2) * GRP + g2 * 64 + (l32 & 3) * 16;
+    const int kq = lane & 15;
+    const int v_off = g2 * GRP + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 +
+                      (kq & 1) * 8;
+
+    f32x16 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;  // running max of s * c (log2 units), lazily raised
+    float l = 0.0f;       // this lane's share of the row sum
+    const float cs = a.c;
+
+    auto block = [&](const unsigned char* kt, const unsigned char* vt, int key0) {
+        constexpr int kAhead = 3;
+        f32x16 s = f32x16{};
+        {
+            frag fk[KS];
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) fk[k] = as_frag<T>(ld16(kt + k_off + k * 128));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                if (ks + kAhead < KS) fk[ks + kAhead] = as_frag<T>(ld16(kt + k_off + (ks + kAhead) * 128));
+                s = Elem<T>::mma(fk[ks], qf[ks], s);
+            }
+        }
+        if (key0 + BN > kend) {
+            const int lim = kend - key0 - 4 * g2;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) < lim) ? s[r] : -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, s[r]);
+        const float m_new = fmaxf(m, pair_max(mx) * cs);
+        const bool grow = m_new > m + kLazyRescale;
+        const float alpha = grow ? fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new) : 1.0f;
+        m = grow ? m_new : m;
+        l *= alpha;
+        if (__ballot(grow) != 0) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+        }
+        const float m_use = (m == -INFINITY) ? 0.0f : m;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], cs, -m_use));
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) sum += s[r] + s[r + 1];
+        l += sum;
+        frag p[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            p[h] = pack_frag<T>(s[8 * h + 0], s[8 * h + 1], s[8 * h + 2], s[8 * h + 3],
+                                s[8 * h + 4], s[8 * h + 5], s[8 * h + 6], s[8 * h + 7]);
+        constexpr int kMma = 2 * NDT;
+        frag fv[kMma];
+        auto v_frag = [&](int i) {
+            const unsigned char* a0 = vt + v_off + 4 * (i / NDT) * GRP + (i % NDT) * 256;
+            return tr_frag_at<T>(a0, a0 + 2 * GRP);
+        };
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) fv[k] = v_frag(k);
+#pragma unroll
+        for (int i = 0; i < kMma; ++i) {
+            if (i + kAhead < kMma) fv[i + kAhead] = v_frag(i + kAhead);
+            o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
+        }
+    };
+
+    // Block j in Kb[j & 1] / Vb[j & 1]; block j + 1's loads are issued once block j's have
+    // landed (vmcnt(0)), into the buffers block j - 1 used (its LDS reads were consumed by its
+    // MFMAs). One wave per workgroup, so no barrier. (A third buffer, two blocks in flight,
+    // measured slower: three workgroups per CU instead of four.)
+    if (nblk > 0) {
+        load_tile(Kh, kbeg, Kb0);
+        load_tile(Vh, kbeg, Vb0);
+    }
+    for (int j = 0; j < nblk; j += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        if (j + 1 < nblk) {
+            load_tile(Kh, kbeg + (j + 1) * BN, Kb1);
+            load_tile(Vh, kbeg + (j + 1) * BN, Vb1);
+        }
+        block(Kb0, Vb0, kbeg + j * BN);
+        if (j + 1 >= nblk) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        if (j + 2 < nblk) {
+            load_tile(Kh, kbeg + (j + 2) * BN, Kb0);
+            load_tile(Vh, kbeg + (j + 2) * BN, Vb0);
+        }
+        block(Kb1, Vb1, kbeg + (j + 1) * BN);
+    }
+
+    // Partials of the query heads of this wave's columns: lane l32 < G holds head h0 + l32,
+    // dims 32 dt + 8 q + 4 g2 .. + 3 in o[dt][4 q .. 4 q + 3].
+    l = pair_sum(l);
+    if (l32 < hpk) {
+        const size_t slot = (static_cast<size_t>(b) * a.H + h0 + l32) * a.nsplit + split;
+        float* dst = part_acc + slot * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                f32x4 w;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) w[u] = o[dt][4 * qq + u];
+                st16(dst + 32 * dt + 8 * qq + 4 * g2, __builtin_bit_cast(u32x4, w));
+            }
+        }
+        if (g2 == 0) part_ml[slot] = make_float2(m, l);
+    }
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(D)
     decode_combine_kernel(const float* __restrict__ part_acc, const float2* __restrict__ part_ml,
@@ -360,17 +574,25 @@ struct FixedScratch {
     size_t bytes;
 };
 
-template <typename T, int D, int G, bool PAGED>
+// MMA: decode_mma_kernel (one workgroup per (batch, key/value head, split) for all the query
+// heads of the key/value head, splits of whole 32-key blocks); else decode_split_kernel with
+// G query heads per workgroup.
+template <typename T, int D, int G, bool PAGED, bool MMA = false>
 FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* L, int B,
                                dev::DecodeArgs a, int num_splits, const FixedScratch& fixed,
                                hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     using Cfg = dev::DecCfg<T, D>;
-    const long long groups = static_cast<long long>(B) * a.Hkv * ((a.H / a.Hkv) / G);
+    const long long groups =
+        static_cast<long long>(B) * a.Hkv * (MMA ? 1 : (a.H / a.Hkv) / G);
     const long long bhq = static_cast<long long>(B) * a.H;
     if (groups > 0x7fffffffLL || bhq > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len);
     a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
+    if constexpr (MMA) {
+        a.chunk = std::max(32, (a.chunk + 31) / 32 * 32);
+        a.nsplit = std::max(1, (a.kv_len + a.chunk - 1) / a.chunk);
+    }
     const long long blocks = groups * a.nsplit;
     const long long slots = bhq * a.nsplit;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
@@ -392,10 +614,18 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(base) + acc_bytes);
 
     int tok = profile_kernel<T, D>("decode_split");
-    launch_kernel(tok, (dev::decode_split_kernel<T, D, G, PAGED>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0, stream,
-                       reinterpret_cast<const E*>(Q), reinterpret_cast<const E*>(K),
-                       reinterpret_cast<const E*>(V), part_acc, part_ml, a);
+    if constexpr (MMA) {
+        static_assert(D == 128 && !PAGED && !std::is_same<T, float>::value, "MMA decode shape");
+        launch_kernel(tok, (dev::decode_mma_kernel<T>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(64), 0, stream, reinterpret_cast<const uint16_t*>(Q),
+                           reinterpret_cast<const uint16_t*>(K),
+                           reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
+    } else {
+        launch_kernel(tok, (dev::decode_split_kernel<T, D, G, PAGED>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0, stream,
+                           reinterpret_cast<const E*>(Q), reinterpret_cast<const E*>(K),
+                           reinterpret_cast<const E*>(V), part_acc, part_ml, a);
+    }
     FlashAttentionError err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
     tok = profile_kernel<T, D>("decode_combine");
@@ -412,6 +642,11 @@ FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O,
                                        const dev::DecodeArgs& a, int num_splits,
                                        const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
+    if constexpr (D == 128 && !PAGED && !std::is_same<T, float>::value) {
+        // 2 to 32 query heads per key/value head: the matrix-core kernel.
+        if (hpk >= 2 && hpk <= 32)
+            return run_decode<T, D, 1, PAGED, true>(Q, K, V, O, L, B, a, num_splits, fx, stream);
+    }
     if (hpk % 8 == 0)
         return run_decode<T, D, 8, PAGED>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     if (hpk % 4 == 0)

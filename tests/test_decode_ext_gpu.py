@@ -128,8 +128,9 @@ def test_decode_paged_empty_sequence(torch_gpu, dtype):
 @pytest.mark.gpu
 def test_decode_gqa_matches_mha_on_repeated_heads(torch_gpu):
     """Grouped-query decode equals the plain decode of the head-repeated keys and values (same
-    library, same split count) up to rounding: a workgroup that carries four query heads keeps
-    fewer key rows in flight per step, so its online-softmax rescales fall elsewhere."""
+    library, same split count) up to rounding: the grouped path (four query heads per key/value
+    head, fp16, head_dim 128) runs the matrix-core kernel, which rounds P to fp16 for P V and
+    rescales in 32-key blocks, where the plain kernel keeps P in fp32."""
     import torch
 
     B, heads, kv_heads, d, n = 2, 16, 4, 128, 3000

@@ -79,3 +79,30 @@ def test_fp16_decode_past_2_31_elements(torch_gpu, splits):
         assert max_abs(lse[b:b + 1, h:h + 1].float().cpu().numpy(), l_ref) <= TOL16, f"L {(b, h)}"
     del q, k, v, o, lse
     torch.cuda.empty_cache()
+
+
+@pytest.mark.gpu
+def test_fp16_gqa_decode_past_2_31_elements(torch_gpu):
+    """Grouped-query decode (32 query heads over 8 key/value heads: the matrix-core kernel) with
+    K and V of 65 x 8 x 32768 x 128 = 2^31 + 2^25 elements each; batch row 64 starts at element
+    2^31. Query heads on both sides of the boundary against the oracle."""
+    torch = torch_gpu
+    B, H, HKV, LKV, D = 65, 32, 8, 32768, 128
+    assert (B - 1) * HKV * LKV * D == 2 ** 31
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(33)
+    q = torch.randn((B, H, 1, D), device=dev, dtype=torch.float16, generator=gen)
+    k = torch.randn((B, HKV, LKV, D), device=dev, dtype=torch.float16, generator=gen)
+    v = torch.randn((B, HKV, LKV, D), device=dev, dtype=torch.float16, generator=gen)
+    o, lse = cuflash_attn.flash_attention_decode(q, k, v, scale=D ** -0.5)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (63, 31), (64, 0), (64, 31)):
+        hk = h // (H // HKV)
+        qh = q[b:b + 1, h:h + 1].float().cpu().numpy().astype(np.float64)
+        kh, vh = (t[b:b + 1, hk:hk + 1].float().cpu().numpy().astype(np.float64) for t in (k, v))
+        o_ref, l_ref = oracle.forward(qh, kh, vh, D ** -0.5, False)
+        assert max_abs(o[b:b + 1, h:h + 1].float().cpu().numpy(), o_ref) <= TOL16, f"O {(b, h)}"
+        assert max_abs(lse[b:b + 1, h:h + 1].float().cpu().numpy(), l_ref) <= TOL16, f"L {(b, h)}"
+    del q, k, v, o, lse
+    torch.cuda.empty_cache()
