@@ -299,9 +299,17 @@ __device__ __forceinline__ typename Elem<T>::frag tr_frag_at(const unsigned char
 // (s_waitcnt vmcnt(0) and a barrier before the data is read, and before a buffer is reused).
 // This lets a kernel rotate buffers with run-time offsets, where the compiler would otherwise
 // wait for every outstanding load before each LDS read. The LDS base goes in as an M0 operand
-// (constraint "{m0}"), so the compiler writes M0 itself and knows that the register is taken;
-// an SALU write of M0 needs one wait state before an LDS DMA that uses it, which the s_nop
-// inside the statement provides whatever the compiler placed in between.
+// (constraint "{m0}"), so the compiler writes M0 itself and knows that the register is taken.
+// The compiler cannot see the memory instruction inside the statement, so it inserts none of
+// the wait states that instruction needs. An SALU write of M0 needs one before an LDS DMA that
+// uses it, which the `s_nop 0` inside the statement provides whatever the compiler placed in
+// between. A VALU write of an SGPR (v_readfirstlane, v_readlane) needs five before a memory
+// instruction reads that SGPR, as M0 or as the scalar base address, or the load can use the
+// register's previous value: the bases and LDS addresses given to these helpers are scalar
+// (SALU) values, and tests/test_code_hazards.py checks every LDS-DMA load of the built library
+// for a VALU write of its SGPRs within five wait states. A base that comes from a lane
+// (v_readlane) needs the five-wait-state form (decode.hip's lds_dma16_nt_s: 1-3% slower in the
+// head_dim-128 and 256 forward and backward kernels).
 __device__ __forceinline__ unsigned lds_address(const void* p) {
     return static_cast<unsigned>(reinterpret_cast<uintptr_t>(
         (const __attribute__((address_space(3))) unsigned char*)(p)));

@@ -299,15 +299,26 @@ __global__ void __launch_bounds__(256)
 
 // LDS-DMA loads (common.hpp's lds_dma16_async / lds_dma16_async_s) with the non-temporal hint:
 // a decode reads each key / value row once, so the stream should not displace cached lines.
+// `s_nop 4` gives the five wait states that a VALU write of the base or M0 needs before the
+// load reads it: the paged base comes from v_readlane / v_readfirstlane (no cost measured in
+// the decode kernels).
 __device__ __forceinline__ void lds_dma16_nt(const void* src, unsigned char* lds_base) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off nt"
                  :
                  : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
                  : "memory");
 }
+// A wave-uniform pointer that the compiler cannot prove uniform, read into SGPRs (lane 0's).
+__device__ __forceinline__ const uint16_t* uniform_ptr(const uint16_t* p) {
+    const uint64_t v = reinterpret_cast<uintptr_t>(p);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+    const uint64_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v >> 32)));
+    return reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>((hi << 32) | lo));
+}
 __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
                                                unsigned char* lds_base) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                  :
                  : "v"(voff), "s"(sbase),
                    "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(lds_base)))
@@ -315,7 +326,7 @@ __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
 }
 
 // ------------------------------------------------------------------------------------------
-// Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 128, contiguous K / V)
+// Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 128)
 // ------------------------------------------------------------------------------------------
 // With several query heads per key/value head, decode_split_kernel is bound by its vector ALU
 // (per key and query head: a 16-lane dot product, its reduction and an 8-wide accumulator
@@ -327,13 +338,16 @@ __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
 // forward's 4-row group layout (K row reads and V transpose reads conflict-free), the next
 // block's loads in flight while the current one is consumed; the split's chunk is a multiple
 // of 32 keys, so only the last block of a sequence is partial (its rows past the end are
-// clamped to the last key and masked). Output: decode_split_kernel's partial (m, l, acc) per
+// clamped to the last key and masked). Paged caches (pages of a multiple of 4 keys, so a 4-row
+// group never crosses a page): each group load is a scalar page base plus a fixed per-lane
+// offset (rows of a page are Hkv D elements apart), with the page indices of the next block
+// fetched one block ahead. Output: decode_split_kernel's partial (m, l, acc) per
 // (query head, split), with m lazily rescaled as in the forward (acc and l always refer to the
 // stored m, so the combine is exact).
 // The LDS (34 KB per workgroup) allows four workgroups, one wave per SIMD; at that register
 // budget the compiler keeps the score and O accumulators in AGPRs (16 v_accvgpr_read per
 // block feed the softmax, O is read back only for a rescale and at the end).
-template <typename T>
+template <typename T, bool PAGED>
 __global__ void __launch_bounds__(64)
     decode_mma_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, float* __restrict__ part_acc,
@@ -362,11 +376,29 @@ __global__ void __launch_bounds__(64)
     const int l32 = lane & 31;
     const int g2 = lane >> 5;
 
+    const int kv_b = PAGED ? min(max(a.seq_lens[b], 0), a.kv_len) : a.kv_len;
     const int kbeg = split * a.chunk;
-    const int kend = min(a.kv_len, kbeg + a.chunk);
+    const int kend = min(kv_b, kbeg + a.chunk);
     const int nblk = kend > kbeg ? (kend - kbeg + BN - 1) / BN : 0;
-    const uint16_t* Kh = K + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
-    const uint16_t* Vh = V + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
+    // Contiguous: key row t of this (batch, key/value head) at Kh + t D. Paged: at
+    // ((page_of(t) page_size + t % page_size) Hkv + hk) D, consecutive rows of a page Hkv D apart.
+    const uint16_t* Kh = PAGED ? K + static_cast<size_t>(hk) * D
+                               : K + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
+    const uint16_t* Vh = PAGED ? V + static_cast<size_t>(hk) * D
+                               : V + (static_cast<size_t>(b) * a.Hkv + hk) * static_cast<size_t>(a.kv_len) * D;
+    auto page_of = [&](int t) {
+        const int j = a.page_shift >= 0 ? t >> a.page_shift : t / a.page_size;
+        return a.block_table[static_cast<size_t>(b) * a.max_pages + j];
+    };
+    // Element offset of key row t from Kh / Vh; `page` is page_of(t) when PAGED.
+    auto row_off = [&](int t, int page) -> size_t {
+        if constexpr (PAGED) {
+            const int r = a.page_shift >= 0 ? t & (a.page_size - 1) : t % a.page_size;
+            return (static_cast<size_t>(page) * a.page_size + r) * static_cast<size_t>(a.Hkv) * D;
+        } else {
+            return static_cast<size_t>(t) * D;
+        }
+    };
 
     // Q^T: lane l32 holds query head h0 + l32 (zeros past the group), dims 16 ks + 8 g2 .. + 8.
     frag qf[KS];
@@ -378,20 +410,38 @@ __global__ void __launch_bounds__(64)
     }
 
     // Tile loads: group g (rows key0 + 4 g .. + 3) by one instruction, lane i: row i % 4,
-    // 16-byte chunk i / 4. Whole tiles use a scalar base; the last one clamps rows to kend - 1.
+    // 16-byte chunk i / 4. Whole tiles use a scalar base per group (paged: the page of group g
+    // is lane g of `pages`); the last one clamps rows to kend - 1 (per-lane addresses).
     const int ld_row = lane & 3;
     const int ld_col = (lane >> 2) * 8;
-    const unsigned ld_voff = static_cast<unsigned>((ld_row * D + ld_col) * 2);
-    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst) {
+    const int row_pitch = PAGED ? a.Hkv * D : D;
+    const unsigned ld_voff = static_cast<unsigned>((ld_row * row_pitch + ld_col) * 2);
+    // Page indices of the groups of the block at key0, lane g holding group g (paged only).
+    auto fetch_pages = [&](int key0) {
+        int pg = 0;
+        if constexpr (PAGED) {
+            if (lane < BN / 4 && key0 + 4 * lane < kend) pg = page_of(key0 + 4 * lane);
+        }
+        return pg;
+    };
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst, int pages) {
         if (key0 + BN <= kend) {
 #pragma unroll
-            for (int g = 0; g < BN / 4; ++g)
-                lds_dma16_nt_s(src + static_cast<size_t>(key0 + 4 * g) * D, ld_voff, dst + g * GRP);
+            for (int g = 0; g < BN / 4; ++g) {
+                if constexpr (PAGED) {
+                    // The base comes from v_readlane and the compiler cannot prove it uniform:
+                    // read it into SGPRs (the load statement's wait states cover the VALU write).
+                    const uint16_t* sb = src + row_off(key0 + 4 * g, __builtin_amdgcn_readlane(pages, g));
+                    lds_dma16_nt_s(uniform_ptr(sb), ld_voff, dst + g * GRP);
+                } else {
+                    lds_dma16_nt_s(src + row_off(key0 + 4 * g, 0), ld_voff, dst + g * GRP);
+                }
+            }
         } else {
 #pragma unroll
             for (int g = 0; g < BN / 4; ++g) {
                 const int row = min(key0 + 4 * g + ld_row, kend - 1);
-                lds_dma16_nt(src + static_cast<size_t>(row) * D + ld_col, dst + g * GRP);
+                lds_dma16_nt(src + row_off(row, PAGED ? page_of(row) : 0) + ld_col, dst + g * GRP);
             }
         }
     };
@@ -469,23 +519,28 @@ __global__ void __launch_bounds__(64)
     // Block j in Kb[j & 1] / Vb[j & 1]; block j + 1's loads are issued once block j's have
     // landed (vmcnt(0)), into the buffers block j - 1 used (its LDS reads were consumed by its
     // MFMAs). One wave per workgroup, so no barrier. (A third buffer, two blocks in flight,
-    // measured slower: three workgroups per CU instead of four.)
+    // measured slower: three workgroups per CU instead of four.) Paged: `pages` holds the page
+    // indices of the next block to load, fetched with the loads of the block before it.
+    int pages = fetch_pages(kbeg);
     if (nblk > 0) {
-        load_tile(Kh, kbeg, Kb0);
-        load_tile(Vh, kbeg, Vb0);
+        load_tile(Kh, kbeg, Kb0, pages);
+        load_tile(Vh, kbeg, Vb0, pages);
+        pages = fetch_pages(kbeg + BN);
     }
     for (int j = 0; j < nblk; j += 2) {
         __builtin_amdgcn_s_waitcnt(0);
         if (j + 1 < nblk) {
-            load_tile(Kh, kbeg + (j + 1) * BN, Kb1);
-            load_tile(Vh, kbeg + (j + 1) * BN, Vb1);
+            load_tile(Kh, kbeg + (j + 1) * BN, Kb1, pages);
+            load_tile(Vh, kbeg + (j + 1) * BN, Vb1, pages);
+            pages = fetch_pages(kbeg + (j + 2) * BN);
         }
         block(Kb0, Vb0, kbeg + j * BN);
         if (j + 1 >= nblk) break;
         __builtin_amdgcn_s_waitcnt(0);
         if (j + 2 < nblk) {
-            load_tile(Kh, kbeg + (j + 2) * BN, Kb0);
-            load_tile(Vh, kbeg + (j + 2) * BN, Vb0);
+            load_tile(Kh, kbeg + (j + 2) * BN, Kb0, pages);
+            load_tile(Vh, kbeg + (j + 2) * BN, Vb0, pages);
+            pages = fetch_pages(kbeg + (j + 3) * BN);
         }
         block(Kb1, Vb1, kbeg + (j + 1) * BN);
     }
@@ -615,8 +670,8 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
 
     int tok = profile_kernel<T, D>("decode_split");
     if constexpr (MMA) {
-        static_assert(D == 128 && !PAGED && !std::is_same<T, float>::value, "MMA decode shape");
-        launch_kernel(tok, (dev::decode_mma_kernel<T>), dim3(static_cast<unsigned>(blocks)),
+        static_assert(D == 128 && !std::is_same<T, float>::value, "MMA decode shape");
+        launch_kernel(tok, (dev::decode_mma_kernel<T, PAGED>), dim3(static_cast<unsigned>(blocks)),
                            dim3(64), 0, stream, reinterpret_cast<const uint16_t*>(Q),
                            reinterpret_cast<const uint16_t*>(K),
                            reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
@@ -642,9 +697,11 @@ FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O,
                                        const dev::DecodeArgs& a, int num_splits,
                                        const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
-    if constexpr (D == 128 && !PAGED && !std::is_same<T, float>::value) {
-        // 2 to 32 query heads per key/value head: the matrix-core kernel.
-        if (hpk >= 2 && hpk <= 32)
+    if constexpr (D == 128 && !std::is_same<T, float>::value) {
+        // 2 to 32 query heads per key/value head (paged: pages of a multiple of 4 keys, and a
+        // per-lane byte offset within a 4-row group, 3 Hkv D 2 + 256, that fits 32 bits): the
+        // matrix-core kernel.
+        if (hpk >= 2 && hpk <= 32 && (!PAGED || (a.page_size % 4 == 0 && a.Hkv <= (1 << 20))))
             return run_decode<T, D, 1, PAGED, true>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     }
     if (hpk % 8 == 0)

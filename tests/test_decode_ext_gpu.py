@@ -100,6 +100,42 @@ def test_decode_paged_parity(torch_gpu, dtype, d, heads, kv_heads, page_size):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 4), (16, 2), (32, 1)])
+@pytest.mark.parametrize("page_size", [4, 12, 6])
+def test_decode_paged_matrix_core_pages(torch_gpu, dtype, heads, kv_heads, page_size):
+    """fp16/bf16 head_dim 128 with 2 to 32 query heads per key/value head runs the matrix-core
+    kernel on pages of a multiple of 4 keys (4: one 4-row group per page; 12: not a power of
+    two) and the vector kernel otherwise (6). Lengths: several 32-key blocks and splits, a
+    partial last block, one key, an empty sequence."""
+    import torch
+
+    B, d, max_pages = 5, 128, (1200 + page_size - 1) // page_size
+    seq_lens = [max_pages * page_size, 1000, 33, 1, 0]
+    k_pool, v_pool, table, seqs = _paged_case(dtype, d, B, heads, kv_heads, page_size, max_pages,
+                                              seq_lens, seed=60 + page_size)
+    q = synth.round_to(synth.normal(61, (B, heads, 1, d)), dtype)
+    tq, tk, tv = (synth.to_torch(x, dtype) for x in (q, k_pool, v_pool))
+    ttab = torch.from_numpy(table).to(tq.device)
+    tlen = torch.tensor(seq_lens, dtype=torch.int32, device=tq.device)
+    group = heads // kv_heads
+    for splits in (0, 3, 16):
+        o, lse = cuflash_attn.flash_attention_decode_paged(tq, tk, tv, ttab, tlen,
+                                                           num_splits=splits)
+        torch.cuda.synchronize()
+        o, lse = synth.to_numpy(o), synth.to_numpy(lse)
+        for b in range(B):
+            if seq_lens[b] == 0:
+                assert np.all(o[b] == 0.0) and np.all(np.isneginf(lse[b]))
+                continue
+            kb, vb = seqs[b]
+            o_ref, l_ref = oracle.forward(q[b:b + 1], _expand_heads(kb[None], group),
+                                          _expand_heads(vb[None], group), d ** -0.5, False)
+            check(dtype, o[b:b + 1], o_ref, f"O b={b} splits={splits}")
+            check(dtype, lse[b:b + 1], l_ref, f"L b={b} splits={splits}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_decode_paged_empty_sequence(torch_gpu, dtype):
     """A sequence of length 0 (or negative) gives O = 0 and L = -inf; the others are unaffected."""
     import torch

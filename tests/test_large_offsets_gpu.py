@@ -1,5 +1,6 @@
 """Tensors past 2^31 elements: the headline path (bf16, head_dim 128, causal forward and
-backward through the reference entry points) and the split-KV decode.
+backward through the reference entry points) and the decodes (split-KV, grouped-query on the
+matrix cores, paged).
 
 Q, K, V, O, dO, dQ, dK and dV each hold 2 x 65568 x 128 x 128 = 2^31 + 2^20 elements (about
 4.3 GB apiece, 35 GB in all), so every head from (1, 65504) on starts past element 2^31 and a
@@ -105,4 +106,43 @@ def test_fp16_gqa_decode_past_2_31_elements(torch_gpu):
         assert max_abs(o[b:b + 1, h:h + 1].float().cpu().numpy(), o_ref) <= TOL16, f"O {(b, h)}"
         assert max_abs(lse[b:b + 1, h:h + 1].float().cpu().numpy(), l_ref) <= TOL16, f"L {(b, h)}"
     del q, k, v, o, lse
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.gpu
+def test_fp16_paged_gqa_decode_past_2_31_elements(torch_gpu):
+    """Paged grouped-query decode (32 query heads over 8 key/value heads, 16-key pages in
+    shuffled order: the matrix-core kernel) over caches of 133120 pages x 16 x 8 x 128 = 2^31 +
+    2^25 elements each: every page from 131072 on lies at or past element 2^31. Sequences whose
+    pages cross that boundary against the oracle on pages gathered in block-table order."""
+    torch = torch_gpu
+    B, H, HKV, PAGE, MAXP, D = 65, 32, 8, 16, 2048, 128
+    npages = B * MAXP
+    assert (npages - 2048) * PAGE * HKV * D == 2 ** 31
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(34)
+    q = torch.randn((B, H, 1, D), device=dev, dtype=torch.float16, generator=gen)
+    kc = torch.randn((npages, PAGE, HKV, D), device=dev, dtype=torch.float16, generator=gen)
+    vc = torch.randn((npages, PAGE, HKV, D), device=dev, dtype=torch.float16, generator=gen)
+    rng = np.random.default_rng(34)
+    table = rng.permutation(npages).reshape(B, MAXP).astype(np.int32)
+    lens = np.full(B, MAXP * PAGE, dtype=np.int32)
+    lens[7] = 20000
+    ttab = torch.from_numpy(table).to(dev)
+    tlen = torch.from_numpy(lens).to(dev)
+    o, lse = cuflash_attn.flash_attention_decode_paged(q, kc, vc, ttab, tlen, scale=D ** -0.5)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (7, 13), (64, 31)):
+        n = int(lens[b])
+        assert table[b, : (n + PAGE - 1) // PAGE].max() >= 131072
+        hk = h // (H // HKV)
+        pages = torch.from_numpy(table[b].astype(np.int64)).to(dev)
+        kh, vh = (t.index_select(0, pages).reshape(MAXP * PAGE, HKV, D)[:n, hk]
+                  .float().cpu().numpy().astype(np.float64) for t in (kc, vc))
+        qh = q[b:b + 1, h:h + 1].float().cpu().numpy().astype(np.float64)
+        o_ref, l_ref = oracle.forward(qh, kh[None, None], vh[None, None], D ** -0.5, False)
+        assert max_abs(o[b:b + 1, h:h + 1].float().cpu().numpy(), o_ref) <= TOL16, f"O {(b, h)}"
+        assert max_abs(lse[b:b + 1, h:h + 1].float().cpu().numpy(), l_ref) <= TOL16, f"L {(b, h)}"
+    del q, kc, vc, o, lse
     torch.cuda.empty_cache()
