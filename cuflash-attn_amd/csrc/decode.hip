@@ -10,7 +10,7 @@
 //   groups and waves are merged at the end. Output: an unnormalized fp32 partial
 //   acc_s = sum_j exp2(s_j - m_s) v_j with m_s (log2 units) and l_s = sum_j exp2(s_j - m_s).
 // decode_combine_kernel: per (batch*head), M = max_s m_s, l = sum_s l_s 2^(m_s - M),
-//   O = sum_s acc_s 2^(m_s - M) / l, L = (M + log2 l) * ln 2.
+//   O = sum_s acc_s 2^(m_s - M) / l, L = (M + log2 l) * ln 2; one workgroup per 32 columns.
 
 #include <mutex>
 
@@ -565,32 +565,81 @@ __global__ void __launch_bounds__(64)
     }
 }
 
+// Upper bound of the split count (choose_splits).
+constexpr int kMaxSplits = 1024;
+
+// One workgroup per (batch*head, 32-column slice of D): its 256 lanes are 8 rows of 32 columns,
+// row r sums the splits r, r + 8, ... of its columns with eight loads in flight per lane, and the
+// split weights 2^(m_s - M) are formed once into LDS. (One lane per column walking every split
+// in sequence was latency-bound at a few heads with hundreds of splits.)
 template <typename T, int D>
-__global__ void __launch_bounds__(D)
+__global__ void __launch_bounds__(256)
     decode_combine_kernel(const float* __restrict__ part_acc, const float2* __restrict__ part_ml,
                           typename Mma<T>::elem* __restrict__ O, float* __restrict__ L,
                           int nsplit) {
-    const int bh = blockIdx.x;
-    const int d = threadIdx.x;
+    constexpr int kSlices = D / 32;
+    constexpr int kRows = 8;
+    constexpr int kInFlight = 8;
+    __shared__ float fw[kMaxSplits];
+    __shared__ float red[4];
+    __shared__ float rows[kRows][33];
+    const int bh = blockIdx.x / kSlices;
+    const int c0 = (blockIdx.x % kSlices) * 32;
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
     const float2* ml = part_ml + static_cast<size_t>(bh) * nsplit;
     const float* acc = part_acc + static_cast<size_t>(bh) * nsplit * D;
+
     float mm = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) mm = fmaxf(mm, ml[s].x);
-    float lt = 0.0f, at = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
+    for (int s = t; s < nsplit; s += 256) mm = fmaxf(mm, ml[s].x);
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) mm = fmaxf(mm, xor_shuffle(mm, k));
+    if ((t & 63) == 0) red[wave] = mm;
+    __syncthreads();
+    mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float lt = 0.0f;
+    for (int s = t; s < nsplit; s += 256) {
         const float2 v = ml[s];
         const float f = exp2_rel(v.x, mm);
+        fw[s] = f;
         lt += v.y * f;
-        at += acc[static_cast<size_t>(s) * D + d] * f;
     }
-    // lt == 0 only when every split was empty (a paged sequence of length 0): O = 0, L = -inf.
-    const float o = lt == 0.0f ? 0.0f : at / lt;
-    if constexpr (std::is_same<T, float>::value) {
-        O[static_cast<size_t>(bh) * D + d] = o;
-    } else {
-        O[static_cast<size_t>(bh) * D + d] = static_cast<uint16_t>(Elem<T>::pack2(o, 0.0f) & 0xffffu);
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) lt += xor_shuffle(lt, k);
+    if ((t & 63) == 0) red[wave] = lt;
+    __syncthreads();
+    lt = (red[0] + red[1]) + (red[2] + red[3]);
+
+    const int col = t & 31;
+    const int row = t >> 5;
+    const float* a0 = acc + c0 + col;
+    float at = 0.0f;
+    int s = row;
+    for (; s + (kInFlight - 1) * kRows < nsplit; s += kInFlight * kRows) {
+        float x[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) x[u] = a0[static_cast<size_t>(s + u * kRows) * D];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) at = fmaf(x[u], fw[s + u * kRows], at);
     }
-    if (d == 0) L[bh] = lt == 0.0f ? -INFINITY : (mm + fast_log2(lt)) * kLn2;
+    for (; s < nsplit; s += kRows) at = fmaf(a0[static_cast<size_t>(s) * D], fw[s], at);
+    rows[row][col] = at;
+    __syncthreads();
+    if (row == 0) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) sum += rows[r][col];
+        // lt == 0 only when every split was empty (a paged sequence of length 0): O = 0, L = -inf.
+        const float o = lt == 0.0f ? 0.0f : sum / lt;
+        const size_t at_o = static_cast<size_t>(bh) * D + c0 + col;
+        if constexpr (std::is_same<T, float>::value) {
+            O[at_o] = o;
+        } else {
+            O[at_o] = static_cast<uint16_t>(Elem<T>::pack2(o, 0.0f) & 0xffffu);
+        }
+        if (c0 == 0 && col == 0) L[bh] = lt == 0.0f ? -INFINITY : (mm + fast_log2(lt)) * kLn2;
+    }
 }
 
 }  // namespace dev
@@ -608,14 +657,15 @@ int device_cu_count() {
     return cus;
 }
 
-// Split count: enough (batch*head, split) workgroups to give every CU several, with chunks of at
-// least 512 keys; an explicit request is clamped to [1, min(1024, ceil(kv_len / 16))].
-int choose_splits(int requested, int BH, int kv_len) {
-    const int max_useful = std::max(1, std::min(1024, (kv_len + 15) / 16));
+// Split count: enough (batch*head, split) workgroups to give every CU per_cu, with chunks of at
+// least min_chunk keys; an explicit request is clamped to [1, min(1024, ceil(kv_len / 16))]
+// (1024 = dev::kMaxSplits, the combine kernel's bound).
+int choose_splits(int requested, int BH, int kv_len, int min_chunk, int per_cu) {
+    const int max_useful = std::max(1, std::min(dev::kMaxSplits, (kv_len + 15) / 16));
     if (requested > 0) return std::min(requested, max_useful);
-    const int target_blocks = 8 * device_cu_count();
+    const int target_blocks = per_cu * device_cu_count();
     int s = (target_blocks + BH - 1) / BH;
-    s = std::min(s, std::max(1, kv_len / 512));
+    s = std::min(s, std::max(1, kv_len / min_chunk));
     return std::max(1, std::min(s, max_useful));
 }
 
@@ -629,6 +679,9 @@ struct FixedScratch {
     size_t bytes;
 };
 
+constexpr int kMmaMinChunk = 128;
+constexpr int kMmaPerCu = 4;
+
 // MMA: decode_mma_kernel (one workgroup per (batch, key/value head, split) for all the query
 // heads of the key/value head, splits of whole 32-key blocks); else decode_split_kernel with
 // G query heads per workgroup.
@@ -641,8 +694,14 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     const long long groups =
         static_cast<long long>(B) * a.Hkv * (MMA ? 1 : (a.H / a.Hkv) / G);
     const long long bhq = static_cast<long long>(B) * a.H;
-    if (groups > 0x7fffffffLL || bhq > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len);
+    if (groups > 0x7fffffffLL || bhq * (D / 32) > 0x7fffffffLL)
+        return FlashAttentionError::INVALID_DIMENSION;
+    // The matrix-core kernel's workgroup is one wave: shorter chunks (4 blocks), so that short
+    // sequences still fill the chip, and 4 workgroups per CU, one round of its occupancy
+    // (grouped-query decode, 16 x 8 key/value heads x 32768 keys: 327 -> 314 us; B = 1,
+    // 2 key/value heads, 32768 keys: 26 -> 19 us).
+    a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len,
+                             MMA ? kMmaMinChunk : 512, MMA ? kMmaPerCu : 8);
     a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
     if constexpr (MMA) {
         a.chunk = std::max(32, (a.chunk + 31) / 32 * 32);
@@ -684,8 +743,8 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     FlashAttentionError err = from_hip(hipGetLastError());
     if (err != FlashAttentionError::SUCCESS) return err;
     tok = profile_kernel<T, D>("decode_combine");
-    launch_kernel(tok, (dev::decode_combine_kernel<T, D>), dim3(static_cast<unsigned>(bhq)),
-                       dim3(D), 0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L,
+    launch_kernel(tok, (dev::decode_combine_kernel<T, D>),
+                       dim3(static_cast<unsigned>(bhq * (D / 32))), dim3(256), 0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L,
                        a.nsplit);
     return from_hip(hipGetLastError());
 }
