@@ -300,8 +300,8 @@ __global__ void __launch_bounds__(256)
 // LDS-DMA loads (common.hpp's lds_dma16_async / lds_dma16_async_s) with the non-temporal hint:
 // a decode reads each key / value row once, so the stream should not displace cached lines.
 // `s_nop 4` gives the five wait states that a VALU write of the base or M0 needs before the
-// load reads it: the paged base comes from v_readlane / v_readfirstlane (no cost measured in
-// the decode kernels).
+// load reads it: the paged base comes from v_readlane / v_readfirstlane (within noise at
+// config-4 size).
 __device__ __forceinline__ void lds_dma16_nt(const void* src, unsigned char* lds_base) {
     asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off nt"
                  :
