@@ -325,6 +325,100 @@ __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
                  : "memory");
 }
 
+// Byte strides of the operand reads in the LDS tile layouts of the matrix-core decode kernels.
+// Group layout (decode_mma_kernel, one head per tile): the forward's 4-row groups of 1088 bytes,
+// chunk c of row r at (r / 4) 1088 + (4 c + r % 4) 16.
+struct DecGroupLayout {
+    static constexpr int kGroup = 1088;
+    static constexpr int kStep = 128;         // K row reads: the next 16 dims
+    static constexpr int kRows16 = 4 * kGroup;  // V transpose reads: 16 keys further
+    static constexpr int kDtile = 256;        // V transpose reads: 32 dims further
+    static constexpr int kRows8 = 2 * kGroup;   // second half of a V operand: 8 keys further
+};
+// Row layout (decode_mma_rows_kernel, four heads per tile): key row r holds the 256-byte rows of
+// the four heads side by side, chunk c of head w at r R + 256 w + 16 c, with R = 1040 for K
+// (the 16 rows of a K row read step 16 bytes through the banks) and 1088 for V (the 4 rows of a
+// 32-lane transpose read step 64 bytes).
+struct DecRowLayout {
+    static constexpr int kRowK = 1040;
+    static constexpr int kRowV = 1088;
+    static constexpr int kStep = 32;
+    static constexpr int kRows16 = 16 * kRowV;
+    static constexpr int kDtile = 64;
+    static constexpr int kRows8 = 8 * kRowV;
+};
+
+// One 32-key block of the matrix-core decode for this wave's query heads (lane l32 = head): the
+// scores S^T = K Q^T, the mask past kend, the lazily rescaled softmax (m in log2 units, l this
+// lane's share of the row sum), and O^T += V^T P^T. kt / vt are the block's K / V tiles, k_off /
+// v_off this lane's operand offsets in layout Lay.
+template <typename T, class Lay>
+__device__ __forceinline__ void decode_mma_block(const unsigned char* kt, const unsigned char* vt,
+                                                 int k_off, int v_off, int key0, int kend,
+                                                 int g2, float cs,
+                                                 const typename Elem<T>::frag (&qf)[8],
+                                                 f32x16 (&o)[4], float& m, float& l) {
+    using frag = typename Elem<T>::frag;
+    constexpr int KS = 8;
+    constexpr int NDT = 4;
+    constexpr int BN = 32;
+    constexpr int kAhead = 3;
+    f32x16 s = f32x16{};
+    {
+        frag fk[KS];
+#pragma unroll
+        for (int k = 0; k < kAhead; ++k) fk[k] = as_frag<T>(ld16(kt + k_off + k * Lay::kStep));
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + kAhead < KS)
+                fk[ks + kAhead] = as_frag<T>(ld16(kt + k_off + (ks + kAhead) * Lay::kStep));
+            s = Elem<T>::mma(fk[ks], qf[ks], s);
+        }
+    }
+    if (key0 + BN > kend) {
+        const int lim = kend - key0 - 4 * g2;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) < lim) ? s[r] : -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, s[r]);
+    const float m_new = fmaxf(m, pair_max(mx) * cs);
+    const bool grow = m_new > m + kLazyRescale;
+    const float alpha = grow ? fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new) : 1.0f;
+    m = grow ? m_new : m;
+    l *= alpha;
+    if (__ballot(grow) != 0) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    }
+    const float m_use = (m == -INFINITY) ? 0.0f : m;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], cs, -m_use));
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) sum += s[r] + s[r + 1];
+    l += sum;
+    frag p[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        p[h] = pack_frag<T>(s[8 * h + 0], s[8 * h + 1], s[8 * h + 2], s[8 * h + 3], s[8 * h + 4],
+                            s[8 * h + 5], s[8 * h + 6], s[8 * h + 7]);
+    constexpr int kMma = 2 * NDT;
+    frag fv[kMma];
+    auto v_frag = [&](int i) {
+        const unsigned char* a0 = vt + v_off + (i / NDT) * Lay::kRows16 + (i % NDT) * Lay::kDtile;
+        return tr_frag_at<T>(a0, a0 + Lay::kRows8);
+    };
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) fv[k] = v_frag(k);
+#pragma unroll
+    for (int i = 0; i < kMma; ++i) {
+        if (i + kAhead < kMma) fv[i + kAhead] = v_frag(i + kAhead);
+        o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 128)
 // ------------------------------------------------------------------------------------------
@@ -460,60 +554,7 @@ __global__ void __launch_bounds__(64)
     const float cs = a.c;
 
     auto block = [&](const unsigned char* kt, const unsigned char* vt, int key0) {
-        constexpr int kAhead = 3;
-        f32x16 s = f32x16{};
-        {
-            frag fk[KS];
-#pragma unroll
-            for (int k = 0; k < kAhead; ++k) fk[k] = as_frag<T>(ld16(kt + k_off + k * 128));
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                if (ks + kAhead < KS) fk[ks + kAhead] = as_frag<T>(ld16(kt + k_off + (ks + kAhead) * 128));
-                s = Elem<T>::mma(fk[ks], qf[ks], s);
-            }
-        }
-        if (key0 + BN > kend) {
-            const int lim = kend - key0 - 4 * g2;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) < lim) ? s[r] : -INFINITY;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, s[r]);
-        const float m_new = fmaxf(m, pair_max(mx) * cs);
-        const bool grow = m_new > m + kLazyRescale;
-        const float alpha = grow ? fast_exp2(m_new == -INFINITY ? 0.0f : m - m_new) : 1.0f;
-        m = grow ? m_new : m;
-        l *= alpha;
-        if (__ballot(grow) != 0) {
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
-        }
-        const float m_use = (m == -INFINITY) ? 0.0f : m;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], cs, -m_use));
-        float sum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) sum += s[r] + s[r + 1];
-        l += sum;
-        frag p[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            p[h] = pack_frag<T>(s[8 * h + 0], s[8 * h + 1], s[8 * h + 2], s[8 * h + 3],
-                                s[8 * h + 4], s[8 * h + 5], s[8 * h + 6], s[8 * h + 7]);
-        constexpr int kMma = 2 * NDT;
-        frag fv[kMma];
-        auto v_frag = [&](int i) {
-            const unsigned char* a0 = vt + v_off + 4 * (i / NDT) * GRP + (i % NDT) * 256;
-            return tr_frag_at<T>(a0, a0 + 2 * GRP);
-        };
-#pragma unroll
-        for (int k = 0; k < kAhead; ++k) fv[k] = v_frag(k);
-#pragma unroll
-        for (int i = 0; i < kMma; ++i) {
-            if (i + kAhead < kMma) fv[i + kAhead] = v_frag(i + kAhead);
-            o[i % NDT] = Elem<T>::mma(fv[i], p[i / NDT], o[i % NDT]);
-        }
+        decode_mma_block<T, DecGroupLayout>(kt, vt, k_off, v_off, key0, kend, g2, cs, qf, o, m, l);
     };
 
     // Block j in Kb[j & 1] / Vb[j & 1]; block j + 1's loads are issued once block j's have
@@ -559,6 +600,162 @@ __global__ void __launch_bounds__(64)
 #pragma unroll
                 for (int u = 0; u < 4; ++u) w[u] = o[dt][4 * qq + u];
                 st16(dst + 32 * dt + 8 * qq + 4 * g2, __builtin_bit_cast(u32x4, w));
+            }
+        }
+        if (g2 == 0) part_ml[slot] = make_float2(m, l);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Paged grouped-query decode on the matrix cores, four key/value heads per workgroup
+// ------------------------------------------------------------------------------------------
+// In the paged layout [page, key, key/value head, D] the rows of one head are 256-byte pieces
+// Hkv D 2 bytes apart, so a wave of decode_mma_kernel streams 256 bytes per key row, where the
+// contiguous layout gives it 8 KB runs (config-4 size: 10% slower with one page per sequence,
+// the same kernel). Here the four waves of a workgroup take four adjacent key/value heads of one
+// (batch, split): each LDS-DMA load fills one key row of all four heads (1 KB contiguous in HBM
+// and in LDS), wave w loading rows 8 w .. 8 w + 7 of each tile, and the waves share the tiles
+// through one barrier per block. The tiles use the row layout (DecRowLayout), 133 KB for the two
+// buffers of K and V, one workgroup per CU; each wave runs decode_mma_block on its own head's
+// 256-byte column. A load is one key row with one scalar row index, clamped to the sequence's
+// last key past its end (masked), so any page size works.
+template <typename T>
+__global__ void __launch_bounds__(256)
+    decode_mma_rows_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                           const uint16_t* __restrict__ V, float* __restrict__ part_acc,
+                           float2* __restrict__ part_ml, DecodeArgs a) {
+    using Lay = DecRowLayout;
+    constexpr int D = 128;
+    constexpr int KS = D / 16;
+    constexpr int NDT = D / 32;
+    constexpr int BN = 32;
+    constexpr int NW = 4;         // waves = key/value heads per workgroup
+    constexpr int RPW = BN / NW;  // rows of each tile that a wave loads
+    using frag = typename Elem<T>::frag;
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb0[BN * Lay::kRowK];
+    __shared__ __attribute__((aligned(1024))) unsigned char Kb1[BN * Lay::kRowK];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb0[BN * Lay::kRowV];
+    __shared__ __attribute__((aligned(1024))) unsigned char Vb1[BN * Lay::kRowV];
+
+    // blockIdx.x = (b * (Hkv / 4) + quad) * nsplit + split; wave w: key/value head 4 quad + w.
+    const int hpk = a.H / a.Hkv;
+    const int nquad = a.Hkv / NW;
+    int rest = blockIdx.x;
+    const int split = rest % a.nsplit;
+    rest /= a.nsplit;
+    const int quad = rest % nquad;
+    const int b = rest / nquad;
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int hk = quad * NW + w;
+    const int h0 = hk * hpk;
+    const int lane = threadIdx.x & 63;
+    const int l32 = lane & 31;
+    const int g2 = lane >> 5;
+
+    const int kv_b = min(max(a.seq_lens[b], 0), a.kv_len);
+    const int kbeg = split * a.chunk;
+    const int kend = min(kv_b, kbeg + a.chunk);
+    const int nblk = kend > kbeg ? (kend - kbeg + BN - 1) / BN : 0;
+    // Key row t of the four heads: Kq + ((page_of(t) page_size + t % page_size) Hkv) D.
+    const uint16_t* Kq = K + static_cast<size_t>(quad) * NW * D;
+    const uint16_t* Vq = V + static_cast<size_t>(quad) * NW * D;
+    auto page_of = [&](int t) {
+        const int j = a.page_shift >= 0 ? t >> a.page_shift : t / a.page_size;
+        return a.block_table[static_cast<size_t>(b) * a.max_pages + j];
+    };
+    auto row_off = [&](int t, int page) -> size_t {
+        const int r = a.page_shift >= 0 ? t & (a.page_size - 1) : t % a.page_size;
+        return (static_cast<size_t>(page) * a.page_size + r) * static_cast<size_t>(a.Hkv) * D;
+    };
+
+    // Q^T: lane l32 holds query head h0 + l32 (zeros past the group), dims 16 ks + 8 g2 .. + 8.
+    frag qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (l32 < hpk) v = ld16(Q + (static_cast<size_t>(b) * a.H + h0 + l32) * D + 16 * ks + 8 * g2);
+        qf[ks] = as_frag<T>(v);
+    }
+
+    // Tile loads: row RPW w + i of the block at key0 (clamped to kend - 1) by one instruction,
+    // lane i: the 16 bytes at 16 i of the row's 1 KB. Its page is lane i of `pages`.
+    const unsigned ld_voff = static_cast<unsigned>(lane * 16);
+    auto fetch_pages = [&](int key0) {
+        int pg = 0;
+        if (lane < RPW && key0 < kend) pg = page_of(min(key0 + RPW * w + lane, kend - 1));
+        return pg;
+    };
+    auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst, int row_bytes,
+                         int pages) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int t = min(key0 + RPW * w + i, kend - 1);
+            // The base comes from v_readlane and the compiler cannot prove it uniform: read it
+            // into SGPRs (the load statement's wait states cover the VALU write).
+            const uint16_t* sb = src + row_off(t, __builtin_amdgcn_readlane(pages, i));
+            lds_dma16_nt_s(uniform_ptr(sb), ld_voff, dst + (RPW * w + i) * row_bytes);
+        }
+    };
+    // Operand offsets in the row layout: K rows (lane l32 = key, chunk 2 ks + g2 of head w) and
+    // the V transpose reads (rows 4 g2 + (lane % 16) / 4, chunks 2 ((lane / 16) % 2) +
+    // (lane % 4) / 2, half lane % 2).
+    const int k_off = l32 * Lay::kRowK + w * 256 + g2 * 16;
+    const int kq = lane & 15;
+    const int v_off = (4 * g2 + (kq >> 2)) * Lay::kRowV + w * 256 +
+                      (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 16 + (kq & 1) * 8;
+
+    f32x16 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+    float m = -INFINITY;
+    float l = 0.0f;
+    const float cs = a.c;
+
+    // Block j in Kb[j & 1] / Vb[j & 1]. Each wave waits for its own loads of block j (vmcnt(0));
+    // the barrier after it makes every wave's loads visible and ends every wave's reads of block
+    // j - 1, whose buffers block j + 1's loads then fill. `pages` holds the page indices of this
+    // wave's rows of the next block to load.
+    int pages = fetch_pages(kbeg);
+    if (nblk > 0) {
+        load_tile(Kq, kbeg, Kb0, Lay::kRowK, pages);
+        load_tile(Vq, kbeg, Vb0, Lay::kRowV, pages);
+        pages = fetch_pages(kbeg + BN);
+    }
+    for (int j = 0; j < nblk; j += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 1 < nblk) {
+            load_tile(Kq, kbeg + (j + 1) * BN, Kb1, Lay::kRowK, pages);
+            load_tile(Vq, kbeg + (j + 1) * BN, Vb1, Lay::kRowV, pages);
+            pages = fetch_pages(kbeg + (j + 2) * BN);
+        }
+        decode_mma_block<T, Lay>(Kb0, Vb0, k_off, v_off, kbeg + j * BN, kend, g2, cs, qf, o, m, l);
+        if (j + 1 >= nblk) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 2 < nblk) {
+            load_tile(Kq, kbeg + (j + 2) * BN, Kb0, Lay::kRowK, pages);
+            load_tile(Vq, kbeg + (j + 2) * BN, Vb0, Lay::kRowV, pages);
+            pages = fetch_pages(kbeg + (j + 3) * BN);
+        }
+        decode_mma_block<T, Lay>(Kb1, Vb1, k_off, v_off, kbeg + (j + 1) * BN, kend, g2, cs, qf, o,
+                                 m, l);
+    }
+
+    // Partials of this wave's query heads: lane l32 < G holds head h0 + l32, dims 32 dt + 8 q +
+    // 4 g2 .. + 3 in o[dt][4 q .. 4 q + 3].
+    l = pair_sum(l);
+    if (l32 < hpk) {
+        const size_t slot = (static_cast<size_t>(b) * a.H + h0 + l32) * a.nsplit + split;
+        float* dst = part_acc + slot * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                f32x4 v;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = o[dt][4 * qq + u];
+                st16(dst + 32 * dt + 8 * qq + 4 * g2, __builtin_bit_cast(u32x4, v));
             }
         }
         if (g2 == 0) part_ml[slot] = make_float2(m, l);
@@ -681,6 +878,7 @@ struct FixedScratch {
 
 constexpr int kMmaMinChunk = 128;
 constexpr int kMmaPerCu = 4;
+constexpr int kRowsPerCu = 1;
 
 // MMA: decode_mma_kernel (one workgroup per (batch, key/value head, split) for all the query
 // heads of the key/value head, splits of whole 32-key blocks); else decode_split_kernel with
@@ -691,8 +889,11 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
                                hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     using Cfg = dev::DecCfg<T, D>;
-    const long long groups =
-        static_cast<long long>(B) * a.Hkv * (MMA ? 1 : (a.H / a.Hkv) / G);
+    // Paged caches with a multiple of 4 key/value heads: decode_mma_rows_kernel, one workgroup
+    // per (batch, 4 key/value heads, split).
+    const bool rows = MMA && PAGED && a.Hkv % 4 == 0;
+    const long long groups = static_cast<long long>(B) * (rows ? a.Hkv / 4 : a.Hkv) *
+                             (MMA ? 1 : (a.H / a.Hkv) / G);
     const long long bhq = static_cast<long long>(B) * a.H;
     if (groups > 0x7fffffffLL || bhq * (D / 32) > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
@@ -701,7 +902,7 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     // (grouped-query decode, 16 x 8 key/value heads x 32768 keys: 327 -> 314 us; B = 1,
     // 2 key/value heads, 32768 keys: 26 -> 19 us).
     a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len,
-                             MMA ? kMmaMinChunk : 512, MMA ? kMmaPerCu : 8);
+                             MMA ? kMmaMinChunk : 512, rows ? kRowsPerCu : (MMA ? kMmaPerCu : 8));
     a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
     if constexpr (MMA) {
         a.chunk = std::max(32, (a.chunk + 31) / 32 * 32);
@@ -730,10 +931,23 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     int tok = profile_kernel<T, D>("decode_split");
     if constexpr (MMA) {
         static_assert(D == 128 && !std::is_same<T, float>::value, "MMA decode shape");
-        launch_kernel(tok, (dev::decode_mma_kernel<T, PAGED>), dim3(static_cast<unsigned>(blocks)),
-                           dim3(64), 0, stream, reinterpret_cast<const uint16_t*>(Q),
-                           reinterpret_cast<const uint16_t*>(K),
-                           reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
+        bool launched = false;
+        if constexpr (PAGED) {
+            if (rows) {
+                launch_kernel(tok, (dev::decode_mma_rows_kernel<T>),
+                                   dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                                   reinterpret_cast<const uint16_t*>(Q),
+                                   reinterpret_cast<const uint16_t*>(K),
+                                   reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
+                launched = true;
+            }
+        }
+        if (!launched)
+            launch_kernel(tok, (dev::decode_mma_kernel<T, PAGED>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream,
+                               reinterpret_cast<const uint16_t*>(Q),
+                               reinterpret_cast<const uint16_t*>(K),
+                               reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
     } else {
         launch_kernel(tok, (dev::decode_split_kernel<T, D, G, PAGED>),
                            dim3(static_cast<unsigned>(blocks)), dim3(Cfg::kThreads), 0, stream,
@@ -757,10 +971,12 @@ FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O,
                                        const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
     if constexpr (D == 128 && !std::is_same<T, float>::value) {
-        // 2 to 32 query heads per key/value head (paged: pages of a multiple of 4 keys, and a
-        // per-lane byte offset within a 4-row group, 3 Hkv D 2 + 256, that fits 32 bits): the
-        // matrix-core kernel.
-        if (hpk >= 2 && hpk <= 32 && (!PAGED || (a.page_size % 4 == 0 && a.Hkv <= (1 << 20))))
+        // 2 to 32 query heads per key/value head: the matrix-core kernels. Paged caches: the
+        // four-head kernel for a multiple of 4 key/value heads (any page size), else the
+        // one-head kernel for pages of a multiple of 4 keys whose per-lane byte offset within a
+        // 4-row group, 3 Hkv D 2 + 256, fits 32 bits.
+        if (hpk >= 2 && hpk <= 32 &&
+            (!PAGED || a.Hkv % 4 == 0 || (a.page_size % 4 == 0 && a.Hkv <= (1 << 20))))
             return run_decode<T, D, 1, PAGED, true>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     }
     if (hpk % 8 == 0)
