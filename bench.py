@@ -80,8 +80,9 @@ def pmc_workload(kind):
     """Short fixed workloads for rocprofv3 --pmc passes (no timing, no output line):
     cfg3 = 2 x (forward + backward) of config 3; cfg1 / cfg2 = 2 x the forward of config 1 / 2;
     cfg5 = 1 x (forward + backward) of config 5; decode = 2 x config-4 decode (auto splits);
-    copy = one device-to-device copy of 1 GiB, the calibration kernel for FETCH_SIZE and
-    WRITE_SIZE."""
+    decode_gqa / decode_paged = 2 x the grouped-query decode at config-4 size (32 query heads
+    over 8 key/value heads; contiguous / 16-key pages in shuffled order); copy = one
+    device-to-device copy of 1 GiB, the calibration kernel for FETCH_SIZE and WRITE_SIZE."""
     import torch
 
     import cuflash_attn
@@ -115,6 +116,27 @@ def pmc_workload(kind):
         v = torch.randn_like(k)
         for _ in range(2):
             cuflash_attn.flash_attention_decode(q, k, v, num_splits=0)
+    elif kind in ("decode_gqa", "decode_paged"):
+        c = CFG4
+        hkv, page = 8, 16
+        q = torch.randn((c["B"], c["H"], 1, c["D"]), device=dev).half()
+        k = torch.randn((c["B"], hkv, c["LKV"], c["D"]), device=dev, dtype=torch.float16)
+        v = torch.randn_like(k)
+        if kind == "decode_gqa":
+            for _ in range(2):
+                cuflash_attn.flash_attention_decode(q, k, v, num_splits=0)
+        else:
+            npages = c["B"] * c["LKV"] // page
+            g = torch.Generator(device=dev)
+            g.manual_seed(6)
+            perm = torch.randperm(npages, generator=g, device=dev)
+            kp, vp = (t.reshape(c["B"], hkv, c["LKV"] // page, page, c["D"]).permute(0, 2, 3, 1, 4)
+                      .reshape(npages, page, hkv, c["D"])[perm].contiguous() for t in (k, v))
+            del k, v
+            table = torch.argsort(perm).to(torch.int32).reshape(c["B"], -1).contiguous()
+            lens = torch.full((c["B"],), c["LKV"], dtype=torch.int32, device=dev)
+            for _ in range(2):
+                cuflash_attn.flash_attention_decode_paged(q, kp, vp, table, lens, num_splits=0)
     torch.cuda.synchronize()
     return 0
 
@@ -132,7 +154,8 @@ def parse():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-ext", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
-    ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "copy"),
+    ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "decode_gqa",
+                                               "decode_paged", "copy"),
                     default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
     ap.add_argument("--cpu-seq", type=int, default=2048,
