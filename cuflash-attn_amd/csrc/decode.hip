@@ -18,6 +18,7 @@
 #include "launch.hpp"
 #include "profile.hpp"
 #include "softmax.hpp"
+#include "tile_groups.hpp"
 
 namespace cuflash {
 namespace dev {
@@ -325,53 +326,48 @@ __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
                  : "memory");
 }
 
-// Byte strides of the operand reads in the LDS tile layouts of the matrix-core decode kernels.
-// Group layout (decode_mma_kernel, one head per tile): the forward's 4-row groups of 1088 bytes,
-// chunk c of row r at (r / 4) 1088 + (4 c + r % 4) 16.
-struct DecGroupLayout {
-    static constexpr int kGroup = 1088;
-    static constexpr int kStep = 128;         // K row reads: the next 16 dims
-    static constexpr int kRows16 = 4 * kGroup;  // V transpose reads: 16 keys further
-    static constexpr int kDtile = 256;        // V transpose reads: 32 dims further
-    static constexpr int kRows8 = 2 * kGroup;   // second half of a V operand: 8 keys further
-};
-// Row layout (decode_mma_rows_kernel, four heads per tile): key row r holds the 256-byte rows of
-// the four heads side by side, chunk c of head w at r R + 256 w + 16 c, with R = 1040 for K
-// (the 16 rows of a K row read step 16 bytes through the banks) and 1088 for V (the 4 rows of a
-// 32-lane transpose read step 64 bytes).
+// LDS tile layouts of the matrix-core decode kernels, in TileGroups' interface (row_base of a
+// K row read plus k_off(ks); tr_off of a V transpose read plus kTrRows16 per 16 keys, dtile_off
+// per 32 dims and kTrHigh for its second half). decode_mma_kernel uses the forward kernels'
+// groups, TileGroups<D>. The row layout of decode_mma_rows_kernel (four heads per tile): key row
+// r holds the 256-byte rows of the four heads side by side, chunk c of head w at r R + 256 w +
+// 16 c, with R = 1040 for K (the 16 rows of a K row read step 16 bytes through the banks) and
+// 1088 for V (the 4 rows of a 32-lane transpose read step 64 bytes).
 struct DecRowLayout {
     static constexpr int kRowK = 1040;
     static constexpr int kRowV = 1088;
-    static constexpr int kStep = 32;
-    static constexpr int kRows16 = 16 * kRowV;
-    static constexpr int kDtile = 64;
-    static constexpr int kRows8 = 8 * kRowV;
+    static constexpr int kTrRows16 = 16 * kRowV;
+    static constexpr int kTrHigh = 8 * kRowV;
+    static constexpr int k_off(int ks) { return ks * 32; }
+    static constexpr int dtile_off(int dt) { return dt * 64; }
 };
 
 // One 32-key block of the matrix-core decode for this wave's query heads (lane l32 = head): the
 // scores S^T = K Q^T, the mask past kend, the lazily rescaled softmax (m in log2 units, l this
-// lane's share of the row sum), and O^T += V^T P^T. kt / vt are the block's K / V tiles, k_off /
-// v_off this lane's operand offsets in layout Lay.
-template <typename T, class Lay>
+// lane's share of the row sum), and O^T += V^T P^T. kt / vt are the block's K / V tiles; k_base
+// (for even and odd k-steps) and v_off are this lane's operand offsets in layout Lay.
+template <typename T, int D, class Lay>
 __device__ __forceinline__ void decode_mma_block(const unsigned char* kt, const unsigned char* vt,
-                                                 int k_off, int v_off, int key0, int kend,
-                                                 int g2, float cs,
-                                                 const typename Elem<T>::frag (&qf)[8],
-                                                 f32x16 (&o)[4], float& m, float& l) {
+                                                 const int (&k_base)[2], int v_off, int key0,
+                                                 int kend, int g2, float cs,
+                                                 const typename Elem<T>::frag (&qf)[D / 16],
+                                                 f32x16 (&o)[D / 32], float& m, float& l) {
     using frag = typename Elem<T>::frag;
-    constexpr int KS = 8;
-    constexpr int NDT = 4;
+    constexpr int KS = D / 16;
+    constexpr int NDT = D / 32;
     constexpr int BN = 32;
     constexpr int kAhead = 3;
     f32x16 s = f32x16{};
     {
         frag fk[KS];
 #pragma unroll
-        for (int k = 0; k < kAhead; ++k) fk[k] = as_frag<T>(ld16(kt + k_off + k * Lay::kStep));
+        for (int k = 0; k < kAhead && k < KS; ++k)
+            fk[k] = as_frag<T>(ld16(kt + k_base[k & 1] + Lay::k_off(k)));
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             if (ks + kAhead < KS)
-                fk[ks + kAhead] = as_frag<T>(ld16(kt + k_off + (ks + kAhead) * Lay::kStep));
+                fk[ks + kAhead] =
+                    as_frag<T>(ld16(kt + k_base[(ks + kAhead) & 1] + Lay::k_off(ks + kAhead)));
             s = Elem<T>::mma(fk[ks], qf[ks], s);
         }
     }
@@ -407,11 +403,12 @@ __device__ __forceinline__ void decode_mma_block(const unsigned char* kt, const 
     constexpr int kMma = 2 * NDT;
     frag fv[kMma];
     auto v_frag = [&](int i) {
-        const unsigned char* a0 = vt + v_off + (i / NDT) * Lay::kRows16 + (i % NDT) * Lay::kDtile;
-        return tr_frag_at<T>(a0, a0 + Lay::kRows8);
+        const unsigned char* a0 =
+            vt + v_off + (i / NDT) * Lay::kTrRows16 + Lay::dtile_off(i % NDT);
+        return tr_frag_at<T>(a0, a0 + Lay::kTrHigh);
     };
 #pragma unroll
-    for (int k = 0; k < kAhead; ++k) fv[k] = v_frag(k);
+    for (int k = 0; k < kAhead && k < kMma; ++k) fv[k] = v_frag(k);
 #pragma unroll
     for (int i = 0; i < kMma; ++i) {
         if (i + kAhead < kMma) fv[i + kAhead] = v_frag(i + kAhead);
@@ -420,7 +417,7 @@ __device__ __forceinline__ void decode_mma_block(const unsigned char* kt, const 
 }
 
 // ------------------------------------------------------------------------------------------
-// Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 128)
+// Grouped-query decode on the matrix cores (fp16 / bf16, head_dim 32, 64, 128)
 // ------------------------------------------------------------------------------------------
 // With several query heads per key/value head, decode_split_kernel is bound by its vector ALU
 // (per key and query head: a 16-lane dot product, its reduction and an 8-wide accumulator
@@ -429,29 +426,32 @@ __device__ __forceinline__ void decode_mma_block(const unsigned char* kt, const 
 // lane per query head (the lanes of columns past G carry zero queries and store nothing), so the
 // vector work per key is the softmax of one score per head. One wave per (batch, key/value head,
 // split) streams the split's keys in 32-key blocks through LDS-DMA double buffers in the
-// forward's 4-row group layout (K row reads and V transpose reads conflict-free), the next
+// forward kernels' group layout, TileGroups<D> (4-row groups at head_dim 128, 8-row groups at
+// 64 and 32; K row reads and V transpose reads conflict-free), the next
 // block's loads in flight while the current one is consumed; the split's chunk is a multiple
 // of 32 keys, so only the last block of a sequence is partial (its rows past the end are
-// clamped to the last key and masked). Paged caches (pages of a multiple of 4 keys, so a 4-row
-// group never crosses a page): each group load is a scalar page base plus a fixed per-lane
+// clamped to the last key and masked). Paged caches (pages of a multiple of the group's rows, so
+// a group never crosses a page): each group load is a scalar page base plus a fixed per-lane
 // offset (rows of a page are Hkv D elements apart), with the page indices of the next block
 // fetched one block ahead. Output: decode_split_kernel's partial (m, l, acc) per
 // (query head, split), with m lazily rescaled as in the forward (acc and l always refer to the
 // stored m, so the combine is exact).
-// The LDS (34 KB per workgroup) allows four workgroups, one wave per SIMD; at that register
-// budget the compiler keeps the score and O accumulators in AGPRs (16 v_accvgpr_read per
-// block feed the softmax, O is read back only for a rescale and at the end).
-template <typename T, bool PAGED>
+// At head_dim 128 the LDS (34 KB per workgroup) allows four workgroups, one wave per SIMD; at
+// that register budget the compiler keeps the score and O accumulators in AGPRs (16
+// v_accvgpr_read per block feed the softmax, O is read back only for a rescale and at the end).
+template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(64)
     decode_mma_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                       const uint16_t* __restrict__ V, float* __restrict__ part_acc,
                       float2* __restrict__ part_ml, DecodeArgs a) {
-    constexpr int D = 128;
-    constexpr int KS = D / 16;   // k-steps of the score MFMA chain
-    constexpr int NDT = D / 32;  // 32-column tiles of O^T
-    constexpr int BN = 32;       // keys per block
-    constexpr int GRP = 1088;    // bytes per 4-row group
-    constexpr int TILE = (BN / 4) * GRP;
+    using G = TileGroups<D>;
+    constexpr int KS = D / 16;         // k-steps of the score MFMA chain
+    constexpr int NDT = D / 32;        // 32-column tiles of O^T
+    constexpr int BN = 32;             // keys per block
+    constexpr int GR = G::kRows;       // rows per group (one load instruction)
+    constexpr int GRP = G::kBytes;     // bytes per group
+    constexpr int NG = BN / GR;        // groups per tile
+    constexpr int TILE = NG * GRP;
     using frag = typename Elem<T>::frag;
     __shared__ __attribute__((aligned(1024))) unsigned char Kb0[TILE];
     __shared__ __attribute__((aligned(1024))) unsigned char Kb1[TILE];
@@ -503,48 +503,47 @@ __global__ void __launch_bounds__(64)
         qf[ks] = as_frag<T>(v);
     }
 
-    // Tile loads: group g (rows key0 + 4 g .. + 3) by one instruction, lane i: row i % 4,
-    // 16-byte chunk i / 4. Whole tiles use a scalar base per group (paged: the page of group g
-    // is lane g of `pages`); the last one clamps rows to kend - 1 (per-lane addresses).
-    const int ld_row = lane & 3;
-    const int ld_col = (lane >> 2) * 8;
+    // Tile loads: group g (rows key0 + GR g .. + GR - 1) by one instruction, lane i: row
+    // G::ld_row(i), 16-byte chunk G::ld_col(i) / 8. Whole tiles use a scalar base per group
+    // (paged: the page of group g is lane g of `pages`); the last one clamps rows to kend - 1
+    // (per-lane addresses).
+    const int ld_row = G::ld_row(lane);
+    const int ld_col = G::ld_col(lane);
     const int row_pitch = PAGED ? a.Hkv * D : D;
     const unsigned ld_voff = static_cast<unsigned>((ld_row * row_pitch + ld_col) * 2);
     // Page indices of the groups of the block at key0, lane g holding group g (paged only).
     auto fetch_pages = [&](int key0) {
         int pg = 0;
         if constexpr (PAGED) {
-            if (lane < BN / 4 && key0 + 4 * lane < kend) pg = page_of(key0 + 4 * lane);
+            if (lane < NG && key0 + GR * lane < kend) pg = page_of(key0 + GR * lane);
         }
         return pg;
     };
     auto load_tile = [&](const uint16_t* src, int key0, unsigned char* dst, int pages) {
         if (key0 + BN <= kend) {
 #pragma unroll
-            for (int g = 0; g < BN / 4; ++g) {
+            for (int g = 0; g < NG; ++g) {
                 if constexpr (PAGED) {
                     // The base comes from v_readlane and the compiler cannot prove it uniform:
                     // read it into SGPRs (the load statement's wait states cover the VALU write).
-                    const uint16_t* sb = src + row_off(key0 + 4 * g, __builtin_amdgcn_readlane(pages, g));
+                    const uint16_t* sb = src + row_off(key0 + GR * g, __builtin_amdgcn_readlane(pages, g));
                     lds_dma16_nt_s(uniform_ptr(sb), ld_voff, dst + g * GRP);
                 } else {
-                    lds_dma16_nt_s(src + row_off(key0 + 4 * g, 0), ld_voff, dst + g * GRP);
+                    lds_dma16_nt_s(src + row_off(key0 + GR * g, 0), ld_voff, dst + g * GRP);
                 }
             }
         } else {
 #pragma unroll
-            for (int g = 0; g < BN / 4; ++g) {
-                const int row = min(key0 + 4 * g + ld_row, kend - 1);
+            for (int g = 0; g < NG; ++g) {
+                const int row = min(key0 + GR * g + ld_row, kend - 1);
                 lds_dma16_nt(src + row_off(row, PAGED ? page_of(row) : 0) + ld_col, dst + g * GRP);
             }
         }
     };
-    // Operand offsets of the forward's layout: K rows (lane l32 = key, chunk 2 ks + g2) and the
-    // V transpose reads (key group i / NDT, dim tile i % NDT).
-    const int k_off = (l32 >> 2) * GRP + g2 * 64 + (l32 & 3) * 16;
-    const int kq = lane & 15;
-    const int v_off = g2 * GRP + (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 64 + (kq >> 2) * 16 +
-                      (kq & 1) * 8;
+    // Operand offsets of the group layout: K rows (lane l32 = key, chunk 2 ks + g2; the
+    // head_dim-64 groups swizzle by the k-step's parity) and the V transpose reads.
+    const int k_base[2] = {G::row_base(lane, 0), G::row_base(lane, 1)};
+    const int v_off = G::tr_off(lane);
 
     f32x16 o[NDT];
 #pragma unroll
@@ -554,7 +553,7 @@ __global__ void __launch_bounds__(64)
     const float cs = a.c;
 
     auto block = [&](const unsigned char* kt, const unsigned char* vt, int key0) {
-        decode_mma_block<T, DecGroupLayout>(kt, vt, k_off, v_off, key0, kend, g2, cs, qf, o, m, l);
+        decode_mma_block<T, D, G>(kt, vt, k_base, v_off, key0, kend, g2, cs, qf, o, m, l);
     };
 
     // Block j in Kb[j & 1] / Vb[j & 1]; block j + 1's loads are issued once block j's have
@@ -700,6 +699,7 @@ __global__ void __launch_bounds__(256)
     // the V transpose reads (rows 4 g2 + (lane % 16) / 4, chunks 2 ((lane / 16) % 2) +
     // (lane % 4) / 2, half lane % 2).
     const int k_off = l32 * Lay::kRowK + w * 256 + g2 * 16;
+    const int k_base[2] = {k_off, k_off};
     const int kq = lane & 15;
     const int v_off = (4 * g2 + (kq >> 2)) * Lay::kRowV + w * 256 +
                       (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 16 + (kq & 1) * 8;
@@ -729,7 +729,8 @@ __global__ void __launch_bounds__(256)
             load_tile(Vq, kbeg + (j + 1) * BN, Vb1, Lay::kRowV, pages);
             pages = fetch_pages(kbeg + (j + 2) * BN);
         }
-        decode_mma_block<T, Lay>(Kb0, Vb0, k_off, v_off, kbeg + j * BN, kend, g2, cs, qf, o, m, l);
+        decode_mma_block<T, D, Lay>(Kb0, Vb0, k_base, v_off, kbeg + j * BN, kend, g2, cs, qf, o, m,
+                                    l);
         if (j + 1 >= nblk) break;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -738,8 +739,8 @@ __global__ void __launch_bounds__(256)
             load_tile(Vq, kbeg + (j + 2) * BN, Vb0, Lay::kRowV, pages);
             pages = fetch_pages(kbeg + (j + 3) * BN);
         }
-        decode_mma_block<T, Lay>(Kb1, Vb1, k_off, v_off, kbeg + (j + 1) * BN, kend, g2, cs, qf, o,
-                                 m, l);
+        decode_mma_block<T, D, Lay>(Kb1, Vb1, k_base, v_off, kbeg + (j + 1) * BN, kend, g2, cs, qf,
+                                    o, m, l);
     }
 
     // Partials of this wave's query heads: lane l32 < G holds head h0 + l32, dims 32 dt + 8 q +
@@ -877,7 +878,10 @@ struct FixedScratch {
 };
 
 constexpr int kMmaMinChunk = 128;
-constexpr int kMmaPerCu = 4;
+// Workgroups per CU that the one-head matrix-core kernel's split count aims at: 4 (its LDS
+// occupancy at head_dim 128); 8 at head_dim 32, whose 512-byte group loads need more workgroups
+// in flight (16 x 8 key/value heads x 32768 keys: 130 -> 89 us; head_dim 64: 156 -> 161 us).
+constexpr int mma_per_cu(int D) { return D == 32 ? 8 : 4; }
 constexpr int kRowsPerCu = 1;
 
 // MMA: decode_mma_kernel (one workgroup per (batch, key/value head, split) for all the query
@@ -891,18 +895,20 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     using Cfg = dev::DecCfg<T, D>;
     // Paged caches with a multiple of 4 key/value heads: decode_mma_rows_kernel, one workgroup
     // per (batch, 4 key/value heads, split).
-    const bool rows = MMA && PAGED && a.Hkv % 4 == 0;
+    const bool rows = MMA && PAGED && D == 128 && a.Hkv % 4 == 0;
     const long long groups = static_cast<long long>(B) * (rows ? a.Hkv / 4 : a.Hkv) *
                              (MMA ? 1 : (a.H / a.Hkv) / G);
     const long long bhq = static_cast<long long>(B) * a.H;
     if (groups > 0x7fffffffLL || bhq * (D / 32) > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
-    // The matrix-core kernel's workgroup is one wave: shorter chunks (4 blocks), so that short
-    // sequences still fill the chip, and 4 workgroups per CU, one round of its occupancy
-    // (grouped-query decode, 16 x 8 key/value heads x 32768 keys: 327 -> 314 us; B = 1,
-    // 2 key/value heads, 32768 keys: 26 -> 19 us).
+    // The one-head matrix-core kernel's workgroup is one wave: shorter chunks (4 blocks), so
+    // that short sequences still fill the chip, and mma_per_cu(D) workgroups per CU
+    // (grouped-query decode, head_dim 128, 16 x 8 key/value heads x 32768 keys: 327 -> 314 us;
+    // B = 1, 2 key/value heads, 32768 keys: 26 -> 19 us). The four-head kernel: one workgroup
+    // per CU (its LDS occupancy).
     a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len,
-                             MMA ? kMmaMinChunk : 512, rows ? kRowsPerCu : (MMA ? kMmaPerCu : 8));
+                             MMA ? kMmaMinChunk : 512,
+                             rows ? kRowsPerCu : (MMA ? mma_per_cu(D) : 8));
     a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
     if constexpr (MMA) {
         a.chunk = std::max(32, (a.chunk + 31) / 32 * 32);
@@ -930,9 +936,10 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
 
     int tok = profile_kernel<T, D>("decode_split");
     if constexpr (MMA) {
-        static_assert(D == 128 && !std::is_same<T, float>::value, "MMA decode shape");
+        static_assert((D == 32 || D == 64 || D == 128) && !std::is_same<T, float>::value,
+                      "MMA decode shape");
         bool launched = false;
-        if constexpr (PAGED) {
+        if constexpr (PAGED && D == 128) {
             if (rows) {
                 launch_kernel(tok, (dev::decode_mma_rows_kernel<T>),
                                    dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
@@ -943,7 +950,7 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
             }
         }
         if (!launched)
-            launch_kernel(tok, (dev::decode_mma_kernel<T, PAGED>),
+            launch_kernel(tok, (dev::decode_mma_kernel<T, D, PAGED>),
                                dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream,
                                reinterpret_cast<const uint16_t*>(Q),
                                reinterpret_cast<const uint16_t*>(K),
@@ -958,8 +965,8 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     if (err != FlashAttentionError::SUCCESS) return err;
     tok = profile_kernel<T, D>("decode_combine");
     launch_kernel(tok, (dev::decode_combine_kernel<T, D>),
-                       dim3(static_cast<unsigned>(bhq * (D / 32))), dim3(256), 0, stream, part_acc, part_ml, reinterpret_cast<E*>(O), L,
-                       a.nsplit);
+                       dim3(static_cast<unsigned>(bhq * (D / 32))), dim3(256), 0, stream, part_acc,
+                       part_ml, reinterpret_cast<E*>(O), L, a.nsplit);
     return from_hip(hipGetLastError());
 }
 
@@ -970,13 +977,16 @@ FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O,
                                        const dev::DecodeArgs& a, int num_splits,
                                        const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
-    if constexpr (D == 128 && !std::is_same<T, float>::value) {
-        // 2 to 32 query heads per key/value head: the matrix-core kernels. Paged caches: the
-        // four-head kernel for a multiple of 4 key/value heads (any page size), else the
-        // one-head kernel for pages of a multiple of 4 keys whose per-lane byte offset within a
-        // 4-row group, 3 Hkv D 2 + 256, fits 32 bits.
+    if constexpr (!std::is_same<T, float>::value) {
+        // 2 to 32 query heads per key/value head: the matrix-core kernels. Paged caches: at
+        // head_dim 128 the four-head kernel for a multiple of 4 key/value heads (any page size),
+        // else the one-head kernel for pages of a multiple of its group's rows (4 at head_dim
+        // 128, 8 at 64 and 32) whose per-lane byte offset within a group, (rows - 1) Hkv D 2 +
+        // 256, fits 32 bits.
+        constexpr int kGroupRows = dev::TileGroups<D>::kRows;
         if (hpk >= 2 && hpk <= 32 &&
-            (!PAGED || a.Hkv % 4 == 0 || (a.page_size % 4 == 0 && a.Hkv <= (1 << 20))))
+            (!PAGED || (D == 128 && a.Hkv % 4 == 0) ||
+             (a.page_size % kGroupRows == 0 && a.Hkv <= (1 << 20))))
             return run_decode<T, D, 1, PAGED, true>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     }
     if (hpk % 8 == 0)

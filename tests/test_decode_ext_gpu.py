@@ -28,7 +28,7 @@ def _expand_heads(x, group):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("heads,kv_heads", [(8, 1), (8, 2), (6, 3), (12, 2), (32, 4), (16, 16)])
 @pytest.mark.parametrize("kv_len", [1, 77, 1500])
 def test_decode_gqa_parity(torch_gpu, dtype, d, heads, kv_heads, kv_len):
@@ -68,7 +68,7 @@ def _paged_case(dtype, d, B, heads, kv_heads, page_size, max_pages, seq_lens, se
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (8, 2), (8, 1)])
 @pytest.mark.parametrize("page_size", [16, 64])
 def test_decode_paged_parity(torch_gpu, dtype, d, heads, kv_heads, page_size):
