@@ -9,6 +9,9 @@
 //   (row-local, no LDS), each lane group folds its rows into a running (m, l, acc) state, and the
 //   groups and waves are merged at the end. Output: an unnormalized fp32 partial
 //   acc_s = sum_j exp2(s_j - m_s) v_j with m_s (log2 units) and l_s = sum_j exp2(s_j - m_s).
+// decode_mma_kernel / decode_mma_rows_kernel: the same partials for 2 to 32 query heads per
+//   key/value head (fp16 / bf16) on the matrix cores, the query heads as the columns of MFMA
+//   tiles; the rows kernel takes four key/value heads of a paged cache per workgroup.
 // decode_combine_kernel: per (batch*head), M = max_s m_s, l = sum_s l_s 2^(m_s - M),
 //   O = sum_s acc_s 2^(m_s - M) / l, L = (M + log2 l) * ln 2; one workgroup per 32 columns.
 
