@@ -332,10 +332,10 @@ __device__ __forceinline__ void lds_dma16_nt_s(const void* sbase, unsigned voff,
 // LDS tile layouts of the matrix-core decode kernels, in TileGroups' interface (row_base of a
 // K row read plus k_off(ks); tr_off of a V transpose read plus kTrRows16 per 16 keys, dtile_off
 // per 32 dims and kTrHigh for its second half). decode_mma_kernel uses the forward kernels'
-// groups, TileGroups<D>. The row layout of decode_mma_rows_kernel (four heads per tile): key row
-// r holds the 256-byte rows of the four heads side by side, chunk c of head w at r R + 256 w +
-// 16 c, with R = 1040 for K (the 16 rows of a K row read step 16 bytes through the banks) and
-// 1088 for V (the 4 rows of a 32-lane transpose read step 64 bytes).
+// groups, TileGroups<D>. The row layout of decode_mma_rows_kernel (512 / D heads per tile): key
+// row r holds the 2D-byte rows of the heads side by side, 1 KB in all, chunk c of head w at r R +
+// 2 D w + 16 c, with R = 1040 for K (the 16 rows of a K row read step 16 bytes through the banks)
+// and 1088 for V (the 4 rows of a 32-lane transpose read step 64 bytes).
 struct DecRowLayout {
     static constexpr int kRowK = 1040;
     static constexpr int kRowV = 1088;
@@ -609,29 +609,29 @@ __global__ void __launch_bounds__(64)
 }
 
 // ------------------------------------------------------------------------------------------
-// Paged grouped-query decode on the matrix cores, four key/value heads per workgroup
+// Paged grouped-query decode on the matrix cores, 1 KB of key/value heads per workgroup
 // ------------------------------------------------------------------------------------------
-// In the paged layout [page, key, key/value head, D] the rows of one head are 256-byte pieces
-// Hkv D 2 bytes apart, so a wave of decode_mma_kernel streams 256 bytes per key row, where the
-// contiguous layout gives it 8 KB runs (config-4 size: 10% slower with one page per sequence,
-// the same kernel). Here the four waves of a workgroup take four adjacent key/value heads of one
-// (batch, split): each LDS-DMA load fills one key row of all four heads (1 KB contiguous in HBM
-// and in LDS), wave w loading rows 8 w .. 8 w + 7 of each tile, and the waves share the tiles
-// through one barrier per block. The tiles use the row layout (DecRowLayout), 133 KB for the two
-// buffers of K and V, one workgroup per CU; each wave runs decode_mma_block on its own head's
-// 256-byte column. A load is one key row with one scalar row index, clamped to the sequence's
-// last key past its end (masked), so any page size works.
-template <typename T>
-__global__ void __launch_bounds__(256)
+// In the paged layout [page, key, key/value head, D] the rows of one head are 2D-byte pieces
+// Hkv D 2 bytes apart, so a wave of decode_mma_kernel streams 2D bytes per key row, where the
+// contiguous layout gives it 8 KB runs (head_dim 128 at config-4 size: 10% slower with one page
+// per sequence, the same kernel). Here the NW = 512 / D waves of a workgroup (4 at head_dim 128,
+// 8 at 64, 16 at 32) take NW adjacent key/value heads of one (batch, split): each LDS-DMA load
+// fills one key row of all NW heads (1 KB contiguous in HBM and in LDS), wave w loading rows
+// RPW w .. RPW w + RPW - 1 of each tile (RPW = 32 / NW), and the waves share the tiles through
+// one barrier per block. The tiles use the row layout (DecRowLayout), 133 KB for the two buffers
+// of K and V, one workgroup per CU; each wave runs decode_mma_block on its own head's 2D-byte
+// column. A load is one key row with one scalar row index, clamped to the sequence's last key
+// past its end (masked), so any page size works.
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * (512 / D))
     decode_mma_rows_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                            const uint16_t* __restrict__ V, float* __restrict__ part_acc,
                            float2* __restrict__ part_ml, DecodeArgs a) {
     using Lay = DecRowLayout;
-    constexpr int D = 128;
     constexpr int KS = D / 16;
     constexpr int NDT = D / 32;
     constexpr int BN = 32;
-    constexpr int NW = 4;         // waves = key/value heads per workgroup
+    constexpr int NW = 512 / D;   // waves = key/value heads per workgroup
     constexpr int RPW = BN / NW;  // rows of each tile that a wave loads
     using frag = typename Elem<T>::frag;
     __shared__ __attribute__((aligned(1024))) unsigned char Kb0[BN * Lay::kRowK];
@@ -639,7 +639,7 @@ __global__ void __launch_bounds__(256)
     __shared__ __attribute__((aligned(1024))) unsigned char Vb0[BN * Lay::kRowV];
     __shared__ __attribute__((aligned(1024))) unsigned char Vb1[BN * Lay::kRowV];
 
-    // blockIdx.x = (b * (Hkv / 4) + quad) * nsplit + split; wave w: key/value head 4 quad + w.
+    // blockIdx.x = (b * (Hkv / NW) + quad) * nsplit + split; wave w: key/value head NW quad + w.
     const int hpk = a.H / a.Hkv;
     const int nquad = a.Hkv / NW;
     int rest = blockIdx.x;
@@ -658,7 +658,7 @@ __global__ void __launch_bounds__(256)
     const int kbeg = split * a.chunk;
     const int kend = min(kv_b, kbeg + a.chunk);
     const int nblk = kend > kbeg ? (kend - kbeg + BN - 1) / BN : 0;
-    // Key row t of the four heads: Kq + ((page_of(t) page_size + t % page_size) Hkv) D.
+    // Key row t of the NW heads: Kq + ((page_of(t) page_size + t % page_size) Hkv) D.
     const uint16_t* Kq = K + static_cast<size_t>(quad) * NW * D;
     const uint16_t* Vq = V + static_cast<size_t>(quad) * NW * D;
     auto page_of = [&](int t) {
@@ -701,10 +701,10 @@ __global__ void __launch_bounds__(256)
     // Operand offsets in the row layout: K rows (lane l32 = key, chunk 2 ks + g2 of head w) and
     // the V transpose reads (rows 4 g2 + (lane % 16) / 4, chunks 2 ((lane / 16) % 2) +
     // (lane % 4) / 2, half lane % 2).
-    const int k_off = l32 * Lay::kRowK + w * 256 + g2 * 16;
+    const int k_off = l32 * Lay::kRowK + w * 2 * D + g2 * 16;
     const int k_base[2] = {k_off, k_off};
     const int kq = lane & 15;
-    const int v_off = (4 * g2 + (kq >> 2)) * Lay::kRowV + w * 256 +
+    const int v_off = (4 * g2 + (kq >> 2)) * Lay::kRowV + w * 2 * D +
                       (2 * ((lane >> 4) & 1) + ((kq & 3) >> 1)) * 16 + (kq & 1) * 8;
 
     f32x16 o[NDT];
@@ -896,10 +896,11 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
                                hipStream_t stream) {
     using E = typename dev::Mma<T>::elem;
     using Cfg = dev::DecCfg<T, D>;
-    // Paged caches with a multiple of 4 key/value heads: decode_mma_rows_kernel, one workgroup
-    // per (batch, 4 key/value heads, split).
-    const bool rows = MMA && PAGED && D == 128 && a.Hkv % 4 == 0;
-    const long long groups = static_cast<long long>(B) * (rows ? a.Hkv / 4 : a.Hkv) *
+    // Paged caches with a multiple of 512 / D key/value heads: decode_mma_rows_kernel, one
+    // workgroup per (batch, 512 / D key/value heads, split).
+    constexpr int kRowHeads = 512 / D;
+    const bool rows = MMA && PAGED && a.Hkv % kRowHeads == 0;
+    const long long groups = static_cast<long long>(B) * (rows ? a.Hkv / kRowHeads : a.Hkv) *
                              (MMA ? 1 : (a.H / a.Hkv) / G);
     const long long bhq = static_cast<long long>(B) * a.H;
     if (groups > 0x7fffffffLL || bhq * (D / 32) > 0x7fffffffLL)
@@ -942,10 +943,11 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
         static_assert((D == 32 || D == 64 || D == 128) && !std::is_same<T, float>::value,
                       "MMA decode shape");
         bool launched = false;
-        if constexpr (PAGED && D == 128) {
+        if constexpr (PAGED) {
             if (rows) {
-                launch_kernel(tok, (dev::decode_mma_rows_kernel<T>),
-                                   dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                launch_kernel(tok, (dev::decode_mma_rows_kernel<T, D>),
+                                   dim3(static_cast<unsigned>(blocks)), dim3(64 * kRowHeads), 0,
+                                   stream,
                                    reinterpret_cast<const uint16_t*>(Q),
                                    reinterpret_cast<const uint16_t*>(K),
                                    reinterpret_cast<const uint16_t*>(V), part_acc, part_ml, a);
@@ -981,14 +983,14 @@ FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O,
                                        const FixedScratch& fx, hipStream_t stream) {
     const int hpk = a.H / a.Hkv;
     if constexpr (!std::is_same<T, float>::value) {
-        // 2 to 32 query heads per key/value head: the matrix-core kernels. Paged caches: at
-        // head_dim 128 the four-head kernel for a multiple of 4 key/value heads (any page size),
-        // else the one-head kernel for pages of a multiple of its group's rows (4 at head_dim
-        // 128, 8 at 64 and 32) whose per-lane byte offset within a group, (rows - 1) Hkv D 2 +
-        // 256, fits 32 bits.
+        // 2 to 32 query heads per key/value head: the matrix-core kernels. Paged caches: the
+        // rows kernel for a multiple of 512 / D key/value heads (any page size), else the
+        // one-head kernel for pages of a multiple of its group's rows (4 at head_dim 128, 8 at
+        // 64 and 32) whose per-lane byte offset within a group, (rows - 1) Hkv D 2 + 256, fits
+        // 32 bits.
         constexpr int kGroupRows = dev::TileGroups<D>::kRows;
         if (hpk >= 2 && hpk <= 32 &&
-            (!PAGED || (D == 128 && a.Hkv % 4 == 0) ||
+            (!PAGED || a.Hkv % (512 / D) == 0 ||
              (a.page_size % kGroupRows == 0 && a.Hkv <= (1 << 20))))
             return run_decode<T, D, 1, PAGED, true>(Q, K, V, O, L, B, a, num_splits, fx, stream);
     }

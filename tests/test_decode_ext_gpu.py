@@ -137,6 +137,43 @@ def test_decode_paged_matrix_core_pages(torch_gpu, dtype, heads, kv_heads, page_
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("group", [2, 8])
+@pytest.mark.parametrize("page_size", [1, 6, 16])
+def test_decode_paged_rows_kernel_head_dims(torch_gpu, dtype, d, group, page_size):
+    """Paged grouped-query decode with 512 / d key/value heads (8 at head_dim 64, 16 at 32): the
+    kernel whose loads read one key row of all of them (1 KB) per instruction, at any page size.
+    Lengths as in test_decode_paged_matrix_core_pages."""
+    import torch
+
+    kv_heads = 512 // d
+    heads = group * kv_heads
+    B, max_pages = 5, (1200 + page_size - 1) // page_size
+    seq_lens = [max_pages * page_size, 1000, 33, 1, 0]
+    k_pool, v_pool, table, seqs = _paged_case(dtype, d, B, heads, kv_heads, page_size, max_pages,
+                                              seq_lens, seed=70 + d + page_size)
+    q = synth.round_to(synth.normal(71, (B, heads, 1, d)), dtype)
+    tq, tk, tv = (synth.to_torch(x, dtype) for x in (q, k_pool, v_pool))
+    ttab = torch.from_numpy(table).to(tq.device)
+    tlen = torch.tensor(seq_lens, dtype=torch.int32, device=tq.device)
+    for splits in (0, 3):
+        o, lse = cuflash_attn.flash_attention_decode_paged(tq, tk, tv, ttab, tlen,
+                                                           num_splits=splits)
+        torch.cuda.synchronize()
+        o, lse = synth.to_numpy(o), synth.to_numpy(lse)
+        for b in range(B):
+            if seq_lens[b] == 0:
+                assert np.all(o[b] == 0.0) and np.all(np.isneginf(lse[b]))
+                continue
+            kb, vb = seqs[b]
+            o_ref, l_ref = oracle.forward(q[b:b + 1], _expand_heads(kb[None], group),
+                                          _expand_heads(vb[None], group), d ** -0.5, False)
+            check(dtype, o[b:b + 1], o_ref, f"O b={b} splits={splits}")
+            check(dtype, lse[b:b + 1], l_ref, f"L b={b} splits={splits}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_decode_paged_empty_sequence(torch_gpu, dtype):
     """A sequence of length 0 (or negative) gives O = 0 and L = -inf; the others are unaffected."""
     import torch
