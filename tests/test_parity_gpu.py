@@ -103,6 +103,28 @@ def test_decode_parity(torch_gpu, dtype, d, kv_len, splits):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("splits,kv_heads", [(1024, 2), (1000, 2), (5000, 2), (700, 1)])
+def test_decode_many_splits(torch_gpu, d, splits, kv_heads):
+    """The combine at 1024 splits per head (the bound of its LDS weight array; larger requests
+    are clamped to it), with a remainder past its 64-split steps (1000), and the matrix-core
+    grouped-query decode when a request asks for chunks shorter than its 32-key blocks (700
+    splits of 16384 keys with 2 query heads per key/value head: 512 splits of 32 keys)."""
+    B, H, kv_len = 1, 2, 16384
+    q = synth.round_to(synth.normal(4, (B, H, 1, d)), "float16")
+    k = synth.round_to(synth.normal(5, (B, kv_heads, kv_len, d)), "float16")
+    v = synth.round_to(synth.normal(6, (B, kv_heads, kv_len, d)), "float16")
+    tq, tk, tv = (synth.to_torch(x, "float16") for x in (q, k, v))
+    o, lse = cuflash_attn.flash_attention_decode(tq, tk, tv, num_splits=splits)
+    torch_gpu.cuda.synchronize()
+    group = H // kv_heads
+    o_ref, l_ref = oracle.forward(q, np.repeat(k, group, axis=1), np.repeat(v, group, axis=1),
+                                  d ** -0.5, False)
+    check("float16", synth.to_numpy(o), o_ref, "O")
+    check("float16", synth.to_numpy(lse), l_ref, "L")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("d", [32, 64])
 @pytest.mark.parametrize("causal", [False, True])
 def test_forward_fp32_both_grids(torch_gpu, d, causal):
