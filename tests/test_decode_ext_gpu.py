@@ -100,12 +100,12 @@ def test_decode_paged_parity(torch_gpu, dtype, d, heads, kv_heads, page_size):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-@pytest.mark.parametrize("heads,kv_heads", [(8, 4), (64, 8), (16, 2), (32, 1)])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 4), (64, 8), (24, 12), (16, 2), (32, 1)])
 @pytest.mark.parametrize("page_size", [4, 12, 6, 1])
 def test_decode_paged_matrix_core_pages(torch_gpu, dtype, heads, kv_heads, page_size):
     """fp16/bf16 head_dim 128 with 2 to 32 query heads per key/value head runs on the matrix
-    cores: with 4 or 8 key/value heads the four-head kernel at every page size (one key row per
-    load), with 1 or 2 the one-head kernel on pages of a multiple of 4 keys (4: one 4-row group
+    cores: with 4, 8 or 12 key/value heads the four-head kernel at every page size (one key row
+    per load; 12: three workgroups per key row), with 1 or 2 the one-head kernel on pages of a multiple of 4 keys (4: one 4-row group
     per page; 12: not a power of two) and the vector kernel otherwise (6, 1). Lengths: several
     32-key blocks and splits, a partial last block, one key, an empty sequence."""
     import torch

@@ -112,3 +112,46 @@ def test_noalloc_validation_matches_decode(lib):
     for args in cases:
         got = fn(*args, None)
         assert got != 0 and got == ref(*args, None), args
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_in_a_captured_graph(torch_gpu, lib):
+    """The entry point that allocates nothing, captured in a HIP graph (torch.cuda.CUDAGraph: its
+    two kernels, no allocation and no memset) and replayed three times, with new queries written
+    into its input and a synchronization between the replays; every replay equals
+    cuflash_attention_decode_f16 run eagerly on the same inputs, bitwise."""
+    torch = torch_gpu
+    b, h, kv_len, d, splits = 2, 8, 4096, 128, 16
+    q, k, v = _inputs(torch, b, h, kv_len, d, 11)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((b, h, 1), float("nan"), device="cuda", dtype=torch.float32)
+    fn = _noalloc(lib)
+
+    def launch():
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        st = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), b, h,
+                kv_len, d, d ** -0.5, splits, stream)
+        assert st == 0, lib.error_string(st)
+
+    # Warm-up on a side stream (the first call on a device looks up the array's address).
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    g = torch.Generator(device="cuda")
+    for rep in range(3):
+        print(f"[noalloc graph] replay {rep}", flush=True)
+        g.manual_seed(100 + rep)
+        q.copy_(torch.randn(q.shape, generator=g, device="cuda", dtype=torch.float32).half())
+        o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        (o_ref, l_ref), _ = _both(torch, lib, q, k, v, splits)
+        assert torch.equal(o, o_ref) and torch.equal(lse, l_ref), f"replay {rep}"
+    del graph
