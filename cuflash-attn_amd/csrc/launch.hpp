@@ -104,17 +104,23 @@ hipMemPool_t workspace_pool();
 // threads on one stream cannot free a buffer the other is about to use; calls on different
 // streams never share one. Up to kStreamCacheBytes per (device, stream) stay allocated until the
 // process ends. hipStreamPerThread names a different stream in every host thread, so it is not
-// cached (stream_cached_buffer returns false).
+// cached (stream_cached_buffer returns false), nor is a stream that is being captured into a
+// graph: every replay of the graph would use the buffer, after later calls had replaced it.
 constexpr size_t kStreamCacheBytes = size_t(64) << 20;
 struct StreamCacheEntry;
 bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
                           std::unique_lock<std::mutex>* lock, FlashAttentionError* err);
 
+// Whether `stream` is being captured into a graph (false if that cannot be determined).
+bool stream_capturing(hipStream_t stream);
+
 // Stream-ordered device workspace, the counterpart of the reference's AsyncFloatBuffer
 // (src/backward/flash_attention_backward_typed.cu:374-394). Either the stream's cached buffer
 // (`cached`, for workspaces of at most kStreamCacheBytes; at most one cached workspace per call)
-// or a per-call hipMallocFromPoolAsync / hipFreeAsync on the caller's stream. Either way the host
-// never synchronizes and concurrent calls on different streams never share memory.
+// or a per-call hipMallocFromPoolAsync / hipFreeAsync on the caller's stream (hipMallocAsync from
+// the device's current pool on a stream that is being captured, which the graph records as an
+// allocation and a free of its own). Either way the host never synchronizes and concurrent calls
+// on different streams never share memory.
 class StreamWorkspace {
 public:
     explicit StreamWorkspace(hipStream_t stream, bool cached = false)
@@ -132,7 +138,7 @@ public:
                 return err;
             }
         }
-        hipMemPool_t pool = workspace_pool();
+        hipMemPool_t pool = stream_capturing(stream_) ? nullptr : workspace_pool();
         hipError_t e = pool ? hipMallocFromPoolAsync(&ptr_, bytes, pool, stream_)
                             : hipMallocAsync(&ptr_, bytes, stream_);
         if (e != hipSuccess) {

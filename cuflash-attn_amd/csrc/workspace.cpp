@@ -69,9 +69,18 @@ std::mutex g_cache_mutex;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamCacheEntry>> g_cache;
 }  // namespace
 
+bool stream_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return status != hipStreamCaptureStatusNone;
+}
+
 bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
                           std::unique_lock<std::mutex>* lock, FlashAttentionError* err) {
-    if (stream == hipStreamPerThread) return false;
+    if (stream == hipStreamPerThread || stream_capturing(stream)) return false;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) {
         (void)hipGetLastError();
