@@ -29,9 +29,12 @@ def _expand_heads(x, group):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (8, 2), (6, 3), (12, 2), (32, 4), (16, 16)])
+@pytest.mark.parametrize("heads,kv_heads", [(8, 1), (8, 2), (6, 3), (12, 2), (32, 4), (16, 16),
+                                            (32, 1), (64, 1)])
 @pytest.mark.parametrize("kv_len", [1, 77, 1500])
 def test_decode_gqa_parity(torch_gpu, dtype, d, heads, kv_heads, kv_len):
+    """Query heads per key/value head: 1 (plain), 2 to 32 (the matrix-core kernels for fp16 /
+    bf16: 32 fills every column of their tiles), 64 (past them: the vector kernel)."""
     B = 2
     q = synth.round_to(synth.normal(11, (B, heads, 1, d)), dtype)
     k = synth.round_to(synth.normal(12, (B, kv_heads, kv_len, d)), dtype)
