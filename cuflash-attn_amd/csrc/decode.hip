@@ -887,9 +887,10 @@ constexpr int kMmaMinChunk = 128;
 constexpr int mma_per_cu(int D) { return D == 32 ? 8 : 4; }
 constexpr int kRowsPerCu = 1;
 
-// MMA: decode_mma_kernel (one workgroup per (batch, key/value head, split) for all the query
-// heads of the key/value head, splits of whole 32-key blocks); else decode_split_kernel with
-// G query heads per workgroup.
+// MMA: the matrix-core kernels, splits of whole 32-key blocks: decode_mma_rows_kernel (paged,
+// one workgroup per (batch, 512 / D key/value heads, split)) or decode_mma_kernel (one
+// workgroup per (batch, key/value head, split)), each for all the query heads of its key/value
+// heads; else decode_split_kernel with G query heads per workgroup.
 template <typename T, int D, int G, bool PAGED, bool MMA = false>
 FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* L, int B,
                                dev::DecodeArgs a, int num_splits, const FixedScratch& fixed,
@@ -975,8 +976,9 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     return from_hip(hipGetLastError());
 }
 
-// G = the largest of 8, 4, 2, 1 that divides the query heads per key/value head: each K/V row
-// is then read once for G query heads.
+// fp16 / bf16 with 2 to 32 query heads per key/value head: the matrix-core kernels (below).
+// Otherwise G = the largest of 8, 4, 2, 1 that divides the query heads per key/value head: each
+// K/V row is then read once for G query heads.
 template <typename T, int D, bool PAGED>
 FlashAttentionError run_decode_grouped(const T* Q, const T* K, const T* V, T* O, float* L, int B,
                                        const dev::DecodeArgs& a, int num_splits,
