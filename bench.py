@@ -20,6 +20,11 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
 * ext: the extended forward / backward (cuflash_attention_{forward,backward}_ext_bf16) on a
   prefill chunk against a KV cache with grouped-query heads, grouped-query training at the
   config-3 size, and head_dim 96 and 256 at the config-3 size; reported beside the headline.
+* sdpa: this library against torch.nn.functional.scaled_dot_product_attention on the same GPU,
+  restricted to its fused flash / memory-efficient kernels: the forward at the shapes of the
+  reference's own SDPA comparison (fp16 causal head_dim 64, docs/performance/benchmarks.md:
+  106-114, where the reference reaches 0.42-0.67x of SDPA on an A100), and config 3's forward +
+  backward; reported beside the headline (speedup = SDPA time / this library's time).
 * cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
   tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
   timed on a bounded sample of the config-3 workload.
@@ -28,7 +33,7 @@ Before the W warmup steps the step runs untimed for --ramp-ms (default 1 s): the
 steps after the inputs are written run 5-10% slower while the GPU's clock settles.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu-baseline]
-                      [--no-decode] [--no-ext] [--no-configs]
+                      [--no-decode] [--no-ext] [--no-configs] [--no-sdpa]
 """
 
 from __future__ import annotations
@@ -153,6 +158,7 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-ext", action="store_true")
+    ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "decode_gqa",
                                                "decode_paged", "copy"),
@@ -178,6 +184,77 @@ EXT_WORKLOADS = [
     ("head_dim_96", 2, 16, 16, 4096, 4096, 96, True),
     ("head_dim_256", 2, 16, 16, 4096, 4096, 256, True),
 ]
+
+
+# The reference's SDPA comparison shapes (docs/performance/benchmarks.md:106-114): fp16, causal,
+# head_dim 64, (batch, heads, seq_len).
+SDPA_SHAPES = [(1, 8, 1024), (8, 16, 1024), (1, 8, 4096), (8, 16, 4096), (1, 8, 8192),
+               (8, 16, 8192), (1, 8, 16384)]
+
+
+def bench_sdpa(torch, steps):
+    """Forward (and config 3's forward + backward) against torch's scaled_dot_product_attention
+    with only its fused flash / memory-efficient kernels allowed (never the math path), as the
+    median of five regions of `steps` calls each, events on the current stream."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    import cuflash_attn
+
+    dev = torch.device("cuda:0")
+    fused = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+
+    def median_ms(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / steps)
+        return sorted(times)[2]
+
+    out = {"torch": torch.__version__, "backends": "flash / memory-efficient only",
+           "reference_on_a100": "0.42x-0.67x of SDPA (forward, these shapes)", "forward": []}
+    try:
+        with sdpa_kernel(fused):
+            for B, H, N in SDPA_SHAPES:
+                q, k, v = (torch.randn((B, H, N, 64), device=dev, dtype=torch.float16)
+                           for _ in range(3))
+                ours = median_ms(lambda: cuflash_attn.flash_attention_forward(q, k, v,
+                                                                              causal=True))
+                ref = median_ms(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True))
+                out["forward"].append({"batch": B, "heads": H, "seq_len": N,
+                                       "ours_ms": round(ours, 4), "sdpa_ms": round(ref, 4),
+                                       "speedup": round(ref / ours, 2)})
+            c = CFG3
+            q, k, v, do = (torch.randn((c["B"], c["H"], c["N"], c["D"]), device=dev,
+                                       dtype=torch.bfloat16) for _ in range(4))
+
+            def ours_step():
+                o, lse = cuflash_attn.flash_attention_forward(q, k, v, causal=True)
+                cuflash_attn.flash_attention_backward(q, k, v, o, lse, do, causal=True)
+
+            qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+            def sdpa_step():
+                o = F.scaled_dot_product_attention(qg, kg, vg, is_causal=True)
+                torch.autograd.grad(o, (qg, kg, vg), do)
+
+            ours = median_ms(ours_step)
+            ref = median_ms(sdpa_step)
+            out["cfg3_fwd_bwd"] = {"workload": "bf16 causal B=2 H=16 N=4096 D=128",
+                                   "ours_ms": round(ours, 4), "sdpa_ms": round(ref, 4),
+                                   "speedup": round(ref / ours, 2)}
+    except RuntimeError as e:  # no fused SDPA kernel for these inputs on this build of torch
+        out["unavailable"] = str(e)[:200]
+    return out
 
 
 def bench_ext(lib, torch, steps, stream):
@@ -483,6 +560,11 @@ def main():
         log("extended forward / backward workloads")
         ext = bench_ext(lib, torch, max(3, args.steps // 4), stream)
 
+    sdpa = None
+    if not args.no_sdpa:
+        log("torch scaled_dot_product_attention (fused kernels) beside this library")
+        sdpa = bench_sdpa(torch, max(5, args.steps // 5))
+
     # ---------------- configs 1, 2 and 5 ----------------
     configs = None
     if not args.no_configs:
@@ -672,6 +754,7 @@ def main():
         "kernel_ms": {kk: round(vv, 4) for kk, vv in k_ms.items()},
         "decode": decode,
         "ext": ext,
+        "sdpa": sdpa,
         "configs": configs,
         "parity": parity,
         "cpu_baseline": cpu,
