@@ -25,6 +25,9 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
   reference's own SDPA comparison (fp16 causal head_dim 64, docs/performance/benchmarks.md:
   106-114, where the reference reaches 0.42-0.67x of SDPA on an A100), and config 3's forward +
   backward; reported beside the headline (speedup = SDPA time / this library's time).
+* reference_shapes: this library's forward and backward at the shapes of the reference's published
+  timing tables (fp16 causal head_dim 64, docs/performance/benchmarks.md:60-96, NVIDIA GPUs,
+  v0.4.0 snapshot), with those published times beside them as context.
 * cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
   tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
   timed on a bounded sample of the config-3 workload.
@@ -34,6 +37,7 @@ steps after the inputs are written run 5-10% slower while the GPU's clock settle
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu-baseline]
                       [--no-decode] [--no-ext] [--no-configs] [--no-sdpa]
+                      [--no-reference-shapes]
 """
 
 from __future__ import annotations
@@ -159,6 +163,7 @@ def parse():
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-ext", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-reference-shapes", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "decode_gqa",
                                                "decode_paged", "copy"),
@@ -255,6 +260,60 @@ def bench_sdpa(torch, steps):
     except RuntimeError as e:  # no fused SDPA kernel for these inputs on this build of torch
         out["unavailable"] = str(e)[:200]
     return out
+
+
+# The reference's published timing tables (docs/performance/benchmarks.md:60-96; fp16, causal,
+# head_dim 64): (batch, heads, seq_len) -> forward ms on A100 / H100, backward ms on A100.
+REFERENCE_SHAPES = [
+    ((1, 8, 1024), {"A100": 0.19, "H100": 0.11}, {"A100": 0.41}),
+    ((1, 8, 4096), {"A100": 2.18, "H100": 1.15}, {"A100": 4.75}),
+    ((1, 8, 8192), {"A100": 7.80, "H100": 3.85}, {"A100": 17.20}),
+    ((1, 8, 16384), {"A100": 28.5, "H100": 13.2}, {"A100": 63.5}),
+    ((16, 16, 4096), {"A100": 65.60, "H100": 34.50}, None),
+    ((1, 16, 32768), {"A100": 205.0, "H100": 88.0}, None),
+]
+
+
+def bench_reference_shapes(torch, steps):
+    """Forward (and backward where the reference publishes one) at the reference's published
+    shapes, median of five regions of `steps` calls, events on the current stream."""
+    import cuflash_attn
+
+    dev = torch.device("cuda:0")
+
+    def median_ms(fn):
+        fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / steps)
+        return sorted(times)[2]
+
+    rows = []
+    for (B, H, N), ref_fwd, ref_bwd in REFERENCE_SHAPES:
+        q, k, v, do = (torch.randn((B, H, N, 64), device=dev, dtype=torch.float16)
+                       for _ in range(4))
+        o, lse = cuflash_attn.flash_attention_forward(q, k, v, causal=True)
+        row = {"batch": B, "heads": H, "seq_len": N,
+               "fwd_ms": round(median_ms(
+                   lambda: cuflash_attn.flash_attention_forward(q, k, v, causal=True)), 4),
+               "reference_fwd_ms": ref_fwd}
+        if ref_bwd:
+            row["bwd_ms"] = round(median_ms(lambda: cuflash_attn.flash_attention_backward(
+                q, k, v, o, lse, do, causal=True)), 4)
+            row["reference_bwd_ms"] = ref_bwd
+        rows.append(row)
+        del q, k, v, do, o, lse
+    return {"note": "the reference's published times are for fp16 causal head_dim 64 on NVIDIA "
+                    "GPUs (v0.4.0 snapshot, docs/performance/benchmarks.md:60-96), reported "
+                    "as context", "rows": rows}
 
 
 def bench_ext(lib, torch, steps, stream):
@@ -560,6 +619,11 @@ def main():
         log("extended forward / backward workloads")
         ext = bench_ext(lib, torch, max(3, args.steps // 4), stream)
 
+    reference_shapes = None
+    if not args.no_reference_shapes:
+        log("the reference's published timing shapes")
+        reference_shapes = bench_reference_shapes(torch, max(3, args.steps // 10))
+
     sdpa = None
     if not args.no_sdpa:
         log("torch scaled_dot_product_attention (fused kernels) beside this library")
@@ -755,6 +819,7 @@ def main():
         "decode": decode,
         "ext": ext,
         "sdpa": sdpa,
+        "reference_shapes": reference_shapes,
         "configs": configs,
         "parity": parity,
         "cpu_baseline": cpu,
