@@ -619,16 +619,6 @@ def main():
         log("extended forward / backward workloads")
         ext = bench_ext(lib, torch, max(3, args.steps // 4), stream)
 
-    reference_shapes = None
-    if not args.no_reference_shapes:
-        log("the reference's published timing shapes")
-        reference_shapes = bench_reference_shapes(torch, max(3, args.steps // 10))
-
-    sdpa = None
-    if not args.no_sdpa:
-        log("torch scaled_dot_product_attention (fused kernels) beside this library")
-        sdpa = bench_sdpa(torch, max(5, args.steps // 5))
-
     # ---------------- configs 1, 2 and 5 ----------------
     configs = None
     if not args.no_configs:
@@ -754,6 +744,17 @@ def main():
                                            f"{page}-key pages in shuffled order")
         decode["extensions"] = dext
         del kp, vp, table, lens, perm
+
+    # ---------------- informational comparisons (after every measured record) ----------
+    reference_shapes = None
+    if not args.no_reference_shapes:
+        log("the reference's published timing shapes")
+        reference_shapes = bench_reference_shapes(torch, max(3, args.steps // 10))
+
+    sdpa = None
+    if not args.no_sdpa:
+        log("torch scaled_dot_product_attention (fused kernels) beside this library")
+        sdpa = bench_sdpa(torch, max(5, args.steps // 5))
 
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
