@@ -28,6 +28,9 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
 * reference_shapes: this library's forward and backward at the shapes of the reference's published
   timing tables (fp16 causal head_dim 64, docs/performance/benchmarks.md:60-96, NVIDIA GPUs,
   v0.4.0 snapshot), with those published times beside them as context.
+* decode_graph: a launch-bound serving step (16 decode calls of 1 sequence, 32 heads, 1024 keys,
+  head_dim 128, fp16) launched eagerly and replayed from captured HIP graphs of the allocating
+  entry point and of the one that allocates nothing: time per call.
 * cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
   tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
   timed on a bounded sample of the config-3 workload.
@@ -37,7 +40,7 @@ steps after the inputs are written run 5-10% slower while the GPU's clock settle
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ramp-ms MS] [--no-cpu-baseline]
                       [--no-decode] [--no-ext] [--no-configs] [--no-sdpa]
-                      [--no-reference-shapes]
+                      [--no-reference-shapes] [--no-decode-graph]
 """
 
 from __future__ import annotations
@@ -164,6 +167,7 @@ def parse():
     ap.add_argument("--no-ext", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-reference-shapes", action="store_true")
+    ap.add_argument("--no-decode-graph", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--pmc-workload", choices=("cfg1", "cfg2", "cfg3", "cfg5", "decode", "decode_gqa",
                                                "decode_paged", "copy"),
@@ -314,6 +318,85 @@ def bench_reference_shapes(torch, steps):
     return {"note": "the reference's published times are for fp16 causal head_dim 64 on NVIDIA "
                     "GPUs (v0.4.0 snapshot, docs/performance/benchmarks.md:60-96), reported "
                     "as context", "rows": rows}
+
+
+def bench_decode_graph(lib, torch, steps):
+    """Per-call time of a launch-bound serving step, 16 small decode calls (distinct inputs per
+    call, as the layers of a step would have), launched eagerly, replayed from a captured graph of
+    the allocating entry point (each captured call records its workspace as a graph allocation and
+    free) and replayed from a captured graph of the entry point that allocates nothing; median of
+    five regions of `steps` steps each."""
+    import ctypes
+
+    import cuflash_attn
+
+    dev = torch.device("cuda:0")
+    calls, B, H, L, D = 16, 1, 32, 1024, 128
+    qs = [torch.randn((B, H, 1, D), device=dev, dtype=torch.float16) for _ in range(calls)]
+    ks = [torch.randn((B, H, L, D), device=dev, dtype=torch.float16) for _ in range(calls)]
+    vs = [torch.randn((B, H, L, D), device=dev, dtype=torch.float16) for _ in range(calls)]
+    outs = [(torch.empty_like(q), torch.empty((B, H, 1), device=dev, dtype=torch.float32))
+            for q in qs]
+    noalloc = lib.library.cuflash_attention_decode_noalloc_f16
+    noalloc.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [ctypes.c_float,
+                                                                     ctypes.c_int, ctypes.c_void_p]
+    noalloc.restype = ctypes.c_int
+
+    def step_alloc():
+        for q, k, v, (o, lse) in zip(qs, ks, vs, outs):
+            cuflash_attn.flash_attention_decode(q, k, v, out=o, lse=lse)
+
+    def step_noalloc():
+        sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for q, k, v, (o, lse) in zip(qs, ks, vs, outs):
+            st = noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                         B, H, L, D, D ** -0.5, 0, sp)
+            if st != 0:
+                raise RuntimeError(f"decode_noalloc status {st}")
+
+    def median_ms(fn):
+        fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / steps)
+        return sorted(times)[2]
+
+    def captured(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph
+
+    res = {"workload": f"{calls} decode calls: fp16 B={B} H={H} Lkv={L} D={D}, auto splits",
+           "eager_us_per_call": round(median_ms(step_alloc) * 1e3 / calls, 2)}
+    step_alloc()
+    torch.cuda.synchronize()
+    ref = [(o.clone(), lse.clone()) for o, lse in outs]
+    for name, fn in (("graph_allocating", step_alloc), ("graph_noalloc", step_noalloc)):
+        graph = captured(fn)
+        res[name + "_us_per_call"] = round(median_ms(graph.replay) * 1e3 / calls, 2)
+        for o, lse in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        res[name + "_equals_eager"] = all(torch.equal(o, r[0]) and torch.equal(lse, r[1])
+                                          for (o, lse), r in zip(outs, ref))
+        del graph
+    return res
 
 
 def bench_ext(lib, torch, steps, stream):
@@ -756,6 +839,11 @@ def main():
         log("torch scaled_dot_product_attention (fused kernels) beside this library")
         sdpa = bench_sdpa(torch, max(5, args.steps // 5))
 
+    decode_graph = None
+    if not args.no_decode_graph:
+        log("decode calls eager and from a captured graph")
+        decode_graph = bench_decode_graph(lib, torch, max(5, args.steps // 5))
+
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
     if not args.no_cpu_baseline:
@@ -821,6 +909,7 @@ def main():
         "ext": ext,
         "sdpa": sdpa,
         "reference_shapes": reference_shapes,
+        "decode_graph": decode_graph,
         "configs": configs,
         "parity": parity,
         "cpu_baseline": cpu,

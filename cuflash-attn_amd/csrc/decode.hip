@@ -880,7 +880,11 @@ struct FixedScratch {
     size_t bytes;
 };
 
-constexpr int kMmaMinChunk = 128;
+// Minimum keys per split of the automatic split count (4 blocks of the matrix-core kernels):
+// short sequences still spread over the chip (512-key chunks -> 128: plain decode, B = 1, 32
+// heads, 1024 keys 13.6 -> 9.0 us; grouped-query, B = 1, 2 key/value heads, 32768 keys 26 ->
+// 19 us; config 4's automatic 4 splits are unaffected).
+constexpr int kMinChunk = 128;
 // Workgroups per CU that the one-head matrix-core kernel's split count aims at: 4 (its LDS
 // occupancy at head_dim 128); 8 at head_dim 32, whose 512-byte group loads need more workgroups
 // in flight (16 x 8 key/value heads x 32768 keys: 130 -> 89 us; head_dim 64: 156 -> 161 us).
@@ -906,13 +910,11 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     const long long bhq = static_cast<long long>(B) * a.H;
     if (groups > 0x7fffffffLL || bhq * (D / 32) > 0x7fffffffLL)
         return FlashAttentionError::INVALID_DIMENSION;
-    // The one-head matrix-core kernel's workgroup is one wave: shorter chunks (4 blocks), so
-    // that short sequences still fill the chip, and mma_per_cu(D) workgroups per CU
-    // (grouped-query decode, head_dim 128, 16 x 8 key/value heads x 32768 keys: 327 -> 314 us;
-    // B = 1, 2 key/value heads, 32768 keys: 26 -> 19 us). The four-head kernel: one workgroup
-    // per CU (its LDS occupancy).
+    // The one-head matrix-core kernel's workgroup is one wave: mma_per_cu(D) workgroups per CU
+    // (grouped-query decode, head_dim 128, 16 x 8 key/value heads x 32768 keys: 8 -> 4 per CU,
+    // 327 -> 314 us). The four-head kernel: one workgroup per CU (its LDS occupancy).
     a.nsplit = choose_splits(num_splits, static_cast<int>(groups), a.kv_len,
-                             MMA ? kMmaMinChunk : 512,
+                             kMinChunk,
                              rows ? kRowsPerCu : (MMA ? mma_per_cu(D) : 8));
     a.chunk = (a.kv_len + a.nsplit - 1) / a.nsplit;
     if constexpr (MMA) {
