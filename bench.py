@@ -829,20 +829,32 @@ def main():
         del kp, vp, table, lens, perm
 
     # ---------------- informational comparisons (after every measured record) ----------
+    # A failure in one of them is recorded in its place and does not cost the JSON line.
+    def informational(label, fn):
+        log(label)
+        try:
+            return fn()
+        except Exception as e:  # noqa: BLE001 - reported, never the headline
+            torch.cuda.synchronize()
+            return {"error": f"{type(e).__name__}: {str(e)[:200]}"}
+
     reference_shapes = None
     if not args.no_reference_shapes:
-        log("the reference's published timing shapes")
-        reference_shapes = bench_reference_shapes(torch, max(3, args.steps // 10))
+        reference_shapes = informational(
+            "the reference's published timing shapes",
+            lambda: bench_reference_shapes(torch, max(3, args.steps // 10)))
 
     sdpa = None
     if not args.no_sdpa:
-        log("torch scaled_dot_product_attention (fused kernels) beside this library")
-        sdpa = bench_sdpa(torch, max(5, args.steps // 5))
+        sdpa = informational(
+            "torch scaled_dot_product_attention (fused kernels) beside this library",
+            lambda: bench_sdpa(torch, max(5, args.steps // 5)))
 
     decode_graph = None
     if not args.no_decode_graph:
-        log("decode calls eager and from a captured graph")
-        decode_graph = bench_decode_graph(lib, torch, max(5, args.steps // 5))
+        decode_graph = informational(
+            "decode calls eager and from a captured graph",
+            lambda: bench_decode_graph(lib, torch, max(5, args.steps // 5)))
 
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
