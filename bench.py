@@ -202,9 +202,10 @@ SDPA_SHAPES = [(1, 8, 1024), (8, 16, 1024), (1, 8, 4096), (8, 16, 4096), (1, 8, 
 
 
 def bench_sdpa(torch, steps):
-    """Forward (and config 3's forward + backward) against torch's scaled_dot_product_attention
-    with only its fused flash / memory-efficient kernels allowed (never the math path), as the
-    median of five regions of `steps` calls each, events on the current stream."""
+    """Forward (and config 3's forward + backward, config 4's decode) against torch's
+    scaled_dot_product_attention with only its fused flash / memory-efficient kernels allowed
+    (never the math path), as the median of five regions of `steps` calls each, events on the
+    current stream."""
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -261,6 +262,18 @@ def bench_sdpa(torch, steps):
             out["cfg3_fwd_bwd"] = {"workload": "bf16 causal B=2 H=16 N=4096 D=128",
                                    "ours_ms": round(ours, 4), "sdpa_ms": round(ref, 4),
                                    "speedup": round(ref / ours, 2)}
+            del q, k, v, do, qg, kg, vg
+            c = CFG4
+            q = torch.randn((c["B"], c["H"], 1, c["D"]), device=dev, dtype=torch.float16)
+            k, v = (torch.randn((c["B"], c["H"], c["LKV"], c["D"]), device=dev,
+                                dtype=torch.float16) for _ in range(2))
+            ours = median_ms(lambda: cuflash_attn.flash_attention_decode(q, k, v, num_splits=16))
+            ref = median_ms(lambda: F.scaled_dot_product_attention(q, k, v))
+            out["cfg4_decode"] = {"workload": "fp16 B=16 H=32 Lkv=32768 D=128, one query "
+                                              "(this library at 16 splits)",
+                                  "ours_ms": round(ours, 4), "sdpa_ms": round(ref, 4),
+                                  "speedup": round(ref / ours, 2)}
+            del q, k, v
     except RuntimeError as e:  # no fused SDPA kernel for these inputs on this build of torch
         out["unavailable"] = str(e)[:200]
     return out
