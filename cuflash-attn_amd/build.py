@@ -54,6 +54,14 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions. forward.hip: LLVM's AMDGPU register-pressure trackers in the machine
+# scheduler. Measured bitwise equal, 1-3% faster for the sequential head_dim-64 forward and level
+# at head_dim 128; in backward.hip the same option spills fewer registers but ran 1% slower.
+SOURCE_FLAGS = {
+    "forward.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
+}
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -62,7 +70,8 @@ def hipcc() -> str:
 
 
 def _compile(src: str, obj: str) -> None:
-    cmd = [hipcc(), "-x", "hip", *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), "-x", "hip", *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), "-c",
+           os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")
