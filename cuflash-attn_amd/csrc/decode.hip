@@ -553,7 +553,7 @@ __global__ void __launch_bounds__(64)
     for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
     float m = -INFINITY;  // running max of s * c (log2 units), lazily raised
     float l = 0.0f;       // this lane's share of the row sum
-    const float cs = a.c;
+    const float cs = fmaxf(a.c, kFltMin);  // scale 0: -inf * 0 would make the masked scores NaN
 
     auto block = [&](const unsigned char* kt, const unsigned char* vt, int key0) {
         decode_mma_block<T, D, G>(kt, vt, k_base, v_off, key0, kend, g2, cs, qf, o, m, l);
@@ -712,7 +712,7 @@ __global__ void __launch_bounds__(64 * (512 / D))
     for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
     float m = -INFINITY;
     float l = 0.0f;
-    const float cs = a.c;
+    const float cs = fmaxf(a.c, kFltMin);  // scale 0: -inf * 0 would make the masked scores NaN
 
     // Block j in Kb[j & 1] / Vb[j & 1]. Each wave waits for its own loads of block j (vmcnt(0));
     // the barrier after it makes every wave's loads visible and ends every wave's reads of block

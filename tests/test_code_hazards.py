@@ -13,6 +13,14 @@ llvm-objdump and checks every LDS-DMA load against both rules, walking back from
 through every control-flow predecessor (fall-through and branches into the window) until five
 wait states are covered. It first checks itself on hand-written listings with and without each
 hazard.
+
+The forward and backward LDS-DMA helpers (common.hpp: lds_dma16_async, lds_dma16_async_s,
+lds_dma4_async) carry a single `s_nop 0`, which covers the SALU write of M0 only. They are safe
+because every base address and LDS address handed to them today is an SALU value (kernel
+arguments, wave-uniform loop counters, readfirstlane of a uniform expression the compiler
+places on the scalar unit). A future call site whose base comes from a lane (v_readlane,
+v_readfirstlane of a divergent value) would need the five-wait-state form that decode.hip's
+helpers use; this test is what catches such a call site, so it must stay in the CPU suite.
 """
 
 from __future__ import annotations

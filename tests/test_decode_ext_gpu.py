@@ -203,6 +203,53 @@ def test_decode_paged_empty_sequence(torch_gpu, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("scale", [0.0, 1e-6, 10.0])
+def test_decode_matrix_core_edge_scales(torch_gpu, dtype, d, scale):
+    """The matrix-core decode kernels at scales validation accepts beyond head_dim^-0.5: zero
+    (uniform attention over the keys; a masked key's -inf score times the scale must not become
+    NaN), tiny and large. Grouped-query contiguous with a key count that leaves a partial last
+    32-key block (decode_mma_kernel), one-head paged (decode_mma_kernel, 2 key/value heads) and
+    four-head paged (decode_mma_rows_kernel, 8 key/value heads) with short sequences."""
+    import torch
+
+    B, heads, kv_heads, n = 2, 16, 4, 77
+    q = synth.round_to(synth.normal(81, (B, heads, 1, d)), dtype)
+    k = synth.round_to(synth.normal(82, (B, kv_heads, n, d)), dtype)
+    v = synth.round_to(synth.normal(83, (B, kv_heads, n, d)), dtype)
+    tq, tk, tv = (synth.to_torch(x, dtype) for x in (q, k, v))
+    for splits in (0, 2):
+        o, lse = cuflash_attn.flash_attention_decode(tq, tk, tv, scale=scale, num_splits=splits)
+        torch.cuda.synchronize()
+        o_ref, l_ref = oracle.forward(q, _expand_heads(k, heads // kv_heads),
+                                      _expand_heads(v, heads // kv_heads), scale, False)
+        check(dtype, synth.to_numpy(o), o_ref, f"O contiguous splits={splits}")
+        check(dtype, synth.to_numpy(lse), l_ref, f"L contiguous splits={splits}")
+
+    for kvh, page_size in ((2, 16), (8, 16)):
+        hq = 4 * kvh
+        seq_lens = [45, 1, 100]
+        max_pages = 7
+        k_pool, v_pool, table, seqs = _paged_case(dtype, d, len(seq_lens), hq, kvh, page_size,
+                                                  max_pages, seq_lens, seed=90 + kvh)
+        qp = synth.round_to(synth.normal(91, (len(seq_lens), hq, 1, d)), dtype)
+        tqp, tkp, tvp = (synth.to_torch(x, dtype) for x in (qp, k_pool, v_pool))
+        ttab = torch.from_numpy(table).to(tqp.device)
+        tlen = torch.tensor(seq_lens, dtype=torch.int32, device=tqp.device)
+        o, lse = cuflash_attn.flash_attention_decode_paged(tqp, tkp, tvp, ttab, tlen,
+                                                           scale=scale, num_splits=0)
+        torch.cuda.synchronize()
+        o, lse = synth.to_numpy(o), synth.to_numpy(lse)
+        for b in range(len(seq_lens)):
+            kb, vb = seqs[b]
+            o_ref, l_ref = oracle.forward(qp[b:b + 1], _expand_heads(kb[None], 4),
+                                          _expand_heads(vb[None], 4), scale, False)
+            check(dtype, o[b:b + 1], o_ref, f"O paged kv_heads={kvh} b={b}")
+            check(dtype, lse[b:b + 1], l_ref, f"L paged kv_heads={kvh} b={b}")
+
+
+@pytest.mark.gpu
 def test_decode_gqa_matches_mha_on_repeated_heads(torch_gpu):
     """Grouped-query decode equals the plain decode of the head-repeated keys and values (same
     library, same split count) up to rounding: the grouped path (four query heads per key/value
