@@ -58,6 +58,10 @@ def _load():
                                           ctypes.c_float, ctypes.c_int, ctypes.c_int]
     lib.cpu_naive_backward_f32.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64,
                                            ctypes.c_float, ctypes.c_int, ctypes.c_int]
+    lib.cpu_naive_rows_f32.argtypes = [_fp, _fp, _fp, _fp, _ip, _i64, _fp, _fp, _fp, _fp, _fp,
+                                       _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int]
+    lib.cpu_naive_decode_f32.argtypes = [_fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64,
+                                         ctypes.c_float, ctypes.c_int]
     _lib = lib
     return lib
 
@@ -190,3 +194,33 @@ def naive_backward_f32(q, k, v, do, scale: float, causal: bool, nthreads: int | 
                                    _ptr(dv), B * H, N, D, float(scale), int(bool(causal)),
                                    nthreads or default_threads())
     return dq, dk, dv
+
+
+def naive_rows_f32(q, k, v, do, scale: float, causal: bool, rows, nthreads: int | None = None):
+    """The naive fp32 forward + backward of one head ([N, D] arrays) restricted to query rows
+    `rows`: O [len(rows), D], L [len(rows)], dQ [len(rows), D], and the selected rows' summed
+    terms of dK and dV [N, D] (the CPU baseline's bounded sample of a long head)."""
+    q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
+    N, D = q.shape
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    r = rows.size
+    o, dq = np.empty((r, D), np.float32), np.empty((r, D), np.float32)
+    lse = np.empty((r,), np.float32)
+    dk, dv = np.empty_like(q), np.empty_like(q)
+    rc = _load().cpu_naive_rows_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(rows), r, _ptr(o),
+                                    _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv), N, D, float(scale),
+                                    int(bool(causal)), nthreads or default_threads())
+    assert rc == 0
+    return o, lse, dq, dk, dv
+
+
+def naive_decode_f32(q, k, v, scale: float, nthreads: int | None = None):
+    """Naive fp32 decode: q [BH, D], k / v [BH, Nk, D] -> O [BH, D], L [BH] (the decode CPU
+    baseline)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    BH, Nk, D = k.shape
+    o = np.empty((BH, D), np.float32)
+    lse = np.empty((BH,), np.float32)
+    _load().cpu_naive_decode_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), BH, Nk, D,
+                                 float(scale), nthreads or default_threads())
+    return o, lse

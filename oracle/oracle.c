@@ -29,6 +29,11 @@
  *                          The reference's naive CPU attention in float arithmetic, exactly as
  *                          written in the two test files above, multithreaded over heads: the
  *                          reported CPU baseline (a port of the reference's CPU path).
+ *   cpu_naive_rows_f32     The same two naive passes restricted to chosen query rows of one
+ *                          head (row i's loops exactly as above, its dK / dV terms summed), so
+ *                          that an evenly spread sample of a long head can be timed.
+ *   cpu_naive_decode_f32   The naive forward's loops at a query length of 1 (the decode CPU
+ *                          baseline; the reference has no decode path).
  *
  * The `mutation` argument (0 = none) plants a known mistake for the tests that check that the
  * pinning checks catch it; it is never non-zero outside those tests:
@@ -571,5 +576,162 @@ int cpu_naive_backward_f32(const float* Q, const float* K, const float* V, const
                            int causal, int nthreads) {
     naive_ctx c = {Q, K, V, dO, NULL, NULL, dQ, dK, dV, N, D, scale, causal};
     parallel_for(BH, nthreads, naive_bwd_heads, &c);
+    return 0;
+}
+
+/* The same naive fp32 forward and backward restricted to the query rows `rows` of one head, so
+ * that a bounded, evenly spread sample of a long head can be timed. Each selected row i does
+ * the work the two functions above do for it, loop for loop: the forward's score row (dot
+ * products for the unmasked keys, exp and normalization over all N keys), O_i and L_i; the
+ * backward's recomputed P row, dP row over all N keys, D_i, dS row, dQ_i (all N keys), and
+ * row i's terms of dV (P_ij dO_i) and dK (dS_ij q_i) for every key j. Rows are split over the
+ * threads; each thread sums its dK / dV terms into its own [N, D] buffers and the buffers are
+ * added at the end. With every row selected the outputs equal cpu_naive_forward_f32 /
+ * cpu_naive_backward_f32 up to the order of the dK / dV sums over i. */
+typedef struct {
+    const float *Q, *K, *V, *dO;
+    const i64* rows;
+    float *O, *L, *dQ, *dK, *dV;
+    float* part; /* nthreads x (dK, dV) x [N, D] */
+    i64 N, D, nrows;
+    float scale;
+    int causal, nthreads;
+} naive_rows_ctx;
+
+static void naive_rows_job(void* p, i64 begin, i64 end) {
+    naive_rows_ctx* c = (naive_rows_ctx*)p;
+    const i64 N = c->N, D = c->D;
+    float* s = (float*)malloc(sizeof(float) * (size_t)N);
+    float* dP = (float*)malloc(sizeof(float) * (size_t)N);
+    for (i64 t = begin; t < end; ++t) {
+        float* pk = c->part + (size_t)t * 2 * (size_t)(N * D);
+        float* pv = pk + N * D;
+        memset(pk, 0, sizeof(float) * (size_t)(2 * N * D));
+        for (i64 r = c->nrows * t / c->nthreads; r < c->nrows * (t + 1) / c->nthreads; ++r) {
+            const i64 i = c->rows[r];
+            const float* qi = c->Q + i * D;
+            const float* doi = c->dO + i * D;
+            /* forward row (naive_fwd_heads) */
+            for (int pass = 0; pass < 2; ++pass) {
+                float max_score = -INFINITY;
+                for (i64 j = 0; j < N; ++j) {
+                    if (c->causal && j > i) {
+                        s[j] = -INFINITY;
+                    } else {
+                        float dot = 0.0f;
+                        for (i64 d = 0; d < D; ++d) dot += qi[d] * c->K[j * D + d];
+                        s[j] = dot * c->scale;
+                    }
+                    if (s[j] > max_score) max_score = s[j];
+                }
+                float sum_exp = 0.0f;
+                for (i64 j = 0; j < N; ++j) {
+                    s[j] = expf(s[j] - max_score);
+                    sum_exp += s[j];
+                }
+                for (i64 j = 0; j < N; ++j) s[j] /= sum_exp;
+                if (pass == 0) {
+                    for (i64 d = 0; d < D; ++d) {
+                        float sum = 0.0f;
+                        for (i64 j = 0; j < N; ++j) sum += s[j] * c->V[j * D + d];
+                        c->O[r * D + d] = sum;
+                    }
+                    c->L[r] = max_score + logf(sum_exp);
+                }
+                /* pass 1 recomputes P as the naive backward does (naive_bwd_heads) */
+            }
+            for (i64 j = 0; j < N; ++j) {
+                float sum = 0.0f;
+                for (i64 d = 0; d < D; ++d) sum += doi[d] * c->V[j * D + d];
+                dP[j] = sum;
+            }
+            float Di = 0.0f;
+            for (i64 j = 0; j < N; ++j) Di += s[j] * dP[j];
+            for (i64 j = 0; j < N; ++j) dP[j] = (c->causal && j > i) ? 0.0f : s[j] * (dP[j] - Di);
+            for (i64 d = 0; d < D; ++d) {
+                float sum = 0.0f;
+                for (i64 j = 0; j < N; ++j) sum += dP[j] * c->K[j * D + d];
+                c->dQ[r * D + d] = sum * c->scale;
+            }
+            for (i64 j = 0; j < N; ++j)
+                for (i64 d = 0; d < D; ++d) {
+                    pv[j * D + d] += s[j] * doi[d];
+                    pk[j * D + d] += dP[j] * qi[d];
+                }
+        }
+    }
+    free(s);
+    free(dP);
+}
+
+int cpu_naive_rows_f32(const float* Q, const float* K, const float* V, const float* dO,
+                       const i64* rows, i64 nrows, float* O, float* L, float* dQ, float* dK,
+                       float* dV, i64 N, i64 D, float scale, int causal, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > nrows) nthreads = (int)(nrows > 0 ? nrows : 1);
+    float* part = (float*)malloc(sizeof(float) * (size_t)nthreads * 2 * (size_t)(N * D));
+    if (!part) return 1;
+    naive_rows_ctx c = {Q, K, V, dO, rows, O, L, dQ, dK, dV, part, N, D, nrows, scale, causal,
+                        nthreads};
+    parallel_for(nthreads, nthreads, naive_rows_job, &c);
+    for (i64 e = 0; e < N * D; ++e) {
+        float k = 0.0f, v = 0.0f;
+        for (int t = 0; t < nthreads; ++t) {
+            k += part[(size_t)t * 2 * (size_t)(N * D) + e];
+            v += part[(size_t)t * 2 * (size_t)(N * D) + N * D + e];
+        }
+        dK[e] = k * scale;
+        dV[e] = v;
+    }
+    free(part);
+    return 0;
+}
+
+/* Naive fp32 decode: one query row per head against Nk keys with the loops of naive_fwd_heads
+ * (scores, max, exp, normalization, P V), heads over the threads. The reported CPU baseline of
+ * the split-KV decode (the reference has no decode path; this is its naive attention at a
+ * query length of 1). */
+typedef struct {
+    const float *Q, *K, *V;
+    float *O, *L;
+    i64 Nk, D;
+    float scale;
+} naive_dec_ctx;
+
+static void naive_dec_heads(void* p, i64 begin, i64 end) {
+    naive_dec_ctx* c = (naive_dec_ctx*)p;
+    const i64 Nk = c->Nk, D = c->D;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)Nk);
+    for (i64 bh = begin; bh < end; ++bh) {
+        const float* q = c->Q + bh * D;
+        const float* Kh = c->K + bh * Nk * D;
+        const float* Vh = c->V + bh * Nk * D;
+        float max_score = -INFINITY;
+        for (i64 j = 0; j < Nk; ++j) {
+            float dot = 0.0f;
+            for (i64 d = 0; d < D; ++d) dot += q[d] * Kh[j * D + d];
+            scores[j] = dot * c->scale;
+            if (scores[j] > max_score) max_score = scores[j];
+        }
+        float sum_exp = 0.0f;
+        for (i64 j = 0; j < Nk; ++j) {
+            scores[j] = expf(scores[j] - max_score);
+            sum_exp += scores[j];
+        }
+        for (i64 j = 0; j < Nk; ++j) scores[j] /= sum_exp;
+        for (i64 d = 0; d < D; ++d) {
+            float sum = 0.0f;
+            for (i64 j = 0; j < Nk; ++j) sum += scores[j] * Vh[j * D + d];
+            c->O[bh * D + d] = sum;
+        }
+        c->L[bh] = max_score + logf(sum_exp);
+    }
+    free(scores);
+}
+
+int cpu_naive_decode_f32(const float* Q, const float* K, const float* V, float* O, float* L,
+                         i64 BH, i64 Nk, i64 D, float scale, int nthreads) {
+    naive_dec_ctx c = {Q, K, V, O, L, Nk, D, scale};
+    parallel_for(BH, nthreads, naive_dec_heads, &c);
     return 0;
 }

@@ -293,6 +293,50 @@ def test_naive_fp32_baseline_agrees():
         np.testing.assert_allclose(a, b, atol=1e-4)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_naive_rows_is_the_naive_baseline_by_rows(causal):
+    """The CPU baseline's row-sampled form: with every query row selected it reproduces the
+    naive forward and backward (O, L, dQ bitwise: the same float loops per row; dK, dV up to
+    the order of their sums over rows, on 1 and 3 threads); a subset of rows gives exactly
+    those rows of O, L and dQ, and dK / dV equal to the selected rows' terms alone (checked
+    against the fp64 oracle with dO zeroed on the other rows)."""
+    N, D = 150, 64
+    q, k, v, do = (synth.normal(90 + i, (1, 1, N, D)) for i in range(4))
+    o, lse = oracle.naive_forward_f32(q, k, v, 0.125, causal)
+    dq, dk, dv = oracle.naive_backward_f32(q, k, v, do, 0.125, causal)
+    for nthreads in (1, 3):
+        ro, rl, rdq, rdk, rdv = oracle.naive_rows_f32(q[0, 0], k[0, 0], v[0, 0], do[0, 0], 0.125,
+                                                      causal, np.arange(N), nthreads=nthreads)
+        np.testing.assert_array_equal(ro, o[0, 0])
+        np.testing.assert_array_equal(rl, lse[0, 0])
+        np.testing.assert_array_equal(rdq, dq[0, 0])
+        np.testing.assert_allclose(rdk, dk[0, 0], atol=2e-6)
+        np.testing.assert_allclose(rdv, dv[0, 0], atol=2e-6)
+    sub = np.arange(3, N, 17)
+    so, sl, sdq, sdk, sdv = oracle.naive_rows_f32(q[0, 0], k[0, 0], v[0, 0], do[0, 0], 0.125,
+                                                  causal, sub, nthreads=2)
+    np.testing.assert_array_equal(so, o[0, 0][sub])
+    np.testing.assert_array_equal(sl, lse[0, 0][sub])
+    np.testing.assert_array_equal(sdq, dq[0, 0][sub])
+    # dV_j = sum_i P_ij dO_i: with dO zero off the selected rows only their terms remain.
+    do_sub = np.zeros_like(do)
+    do_sub[0, 0, sub] = do[0, 0, sub]
+    _, _, dv_ref = oracle.backward(q, k, v, do_sub, 0.125, causal)
+    np.testing.assert_allclose(sdv, dv_ref[0, 0], atol=2e-5)
+    assert np.abs(sdk).max() > 0
+
+
+def test_naive_decode_baseline_agrees():
+    """The decode CPU baseline equals the oracle's forward at a query length of 1."""
+    BH, Nk, D = 5, 700, 64
+    q = synth.normal(95, (BH, D))
+    k, v = synth.normal(96, (BH, Nk, D)), synth.normal(97, (BH, Nk, D))
+    o, lse = oracle.naive_decode_f32(q, k, v, 0.125, nthreads=2)
+    o_ref, l_ref = oracle.forward(q[:, None, None, :], k[:, None], v[:, None], 0.125, False)
+    np.testing.assert_allclose(o, o_ref.reshape(BH, D), atol=2e-6)
+    np.testing.assert_allclose(lse, l_ref.reshape(BH), atol=2e-6)
+
+
 # ------------------------------------------------------------------------------------------
 # separate query / key lengths (Q [B,H,Nq,D], K/V [B,H,Nk,D]; causal: j <= i + Nk - Nq)
 # ------------------------------------------------------------------------------------------
