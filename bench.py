@@ -14,9 +14,12 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
 * Decode (config 4: fp16, B=16 H=32, 1 query, 32768 keys, D=128) is timed for 16/32/64 splits
   (the headline: the best of these, config 4's range) and the library's automatic choice
   (reported beside it); GB/s counts K and V read once plus Q read, O and L written.
-* roofline: the dominant kernel of the step, timed live with HIP events recorded around each of
-  its launches on the launch stream (cuflash_profile_enable), against MI355X's dense bf16 MFMA
-  peak. `rooflines` lists every kernel the same way.
+* roofline: the dominant kernel of the step against MI355X's dense bf16 MFMA peak, timed live on
+  the launch stream: the forward from back-to-back forward calls between two HIP events, the
+  backward's main kernel from back-to-back backward calls minus the delta kernel's time (HIP
+  events around each of its launches, cuflash_profile_enable). `rooflines` lists each kernel
+  with the per-launch event-pair figure beside it; `traffic` is the committed rocprofv3
+  FETCH_SIZE / WRITE_SIZE figure (profiles/hbm_traffic_pmc.md), not a measurement of this run.
 * ext: the extended forward / backward (cuflash_attention_{forward,backward}_ext_bf16) on a
   prefill chunk against a KV cache with grouped-query heads, grouped-query training at the
   config-3 size, and head_dim 96 and 256 at the config-3 size; reported beside the headline.
@@ -32,8 +35,10 @@ Metric: "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM
   head_dim 128, fp16) launched eagerly and replayed from captured HIP graphs of the allocating
   entry point and of the one that allocates nothing: time per call.
 * cpu_baseline: the reference's naive O(N^2) CPU attention (tests/unit/test_forward.cu:21-118,
-  tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, one thread per head,
-  timed on a bounded sample of the config-3 workload.
+  tests/unit/test_backward.cu:21-127) restated in C, float arithmetic, on this box's host cores
+  (the threads used and sched_getaffinity's count are both printed): whole heads of config 3
+  itself at N=4096 (scaled by B*H / heads), one thread on every 16th row of one head, and 16 of
+  config 4's decode rows; see cpu_baseline().
 
 Before the W warmup steps the step runs untimed for --ramp-ms (default 1 s): the first few dozen
 steps after the inputs are written run 5-10% slower while the GPU's clock settles.
@@ -173,10 +178,10 @@ def parse():
                                                "decode_paged", "copy"),
                     default=None,
                     help="run only a short fixed workload for rocprofv3 --pmc passes")
-    ap.add_argument("--cpu-seq", type=int, default=2048,
-                    help="sequence length of the CPU baseline sample (default 2048)")
-    ap.add_argument("--cpu-heads", type=int, default=0,
-                    help="heads in the CPU-baseline sample (default: one per host thread, <= 16)")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="wall time the multi-threaded CPU-baseline sample aims for: whole "
+                         "config-3 heads are timed one after another until this much time has "
+                         "passed (at most 8 heads; default 8 s)")
     return ap.parse_args()
 
 
@@ -555,12 +560,97 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def host_threads():
+def host_cpus():
+    """Host CPUs this process may run on (sched_getaffinity), uncapped."""
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def host_threads():
+    """Threads of the CPU-side work: the host CPUs, at most 16 (the GPU box's CPU share)."""
+    return max(1, min(16, host_cpus()))
+
+
+def cpu_baseline(host, B, H, N, D, scale, causal, target_s, with_decode):
+    """The reference's naive O(N^2) fp32 CPU attention (tests/unit/test_forward.cu:21-118 and
+    tests/unit/test_backward.cu:21-127, restated in oracle.c) timed on this box's host cores on
+    a bounded sample of the config-3 workload itself, and on a sample of config 4.
+
+    Config 3: whole heads of the timed GPU inputs (the same bf16 values, as float32), each
+    head's forward + backward split by query rows over the threads (oracle.naive_rows_f32:
+    row i's loops exactly as in the naive code), timed head after head until `target_s` has
+    passed (at most 8 heads), then scaled by B * H / heads. One thread: every 16th query row of
+    one head, scaled by N / rows (the naive loops do almost the same work for every row: all N
+    keys, except the score dot products of masked keys) and by B * H. The rates use the GPU
+    line's FLOP model, so gpu_speedup compares the same problem.
+    Config 4: 16 of its 512 (batch, head) rows at 32768 keys (fp32 copies of N(0,1) data),
+    median of 5 calls; GB/s counts config 4's algorithmic (fp16) bytes of those rows."""
+    import numpy as np
+
+    import oracle
+
+    threads = host_threads()
+    f_total = 3.5 * flops_fwd(B, H, N, D, causal)
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    rows_all = np.arange(N, dtype=np.int64)
+    log(f"CPU baseline: naive fp32 fwd+bwd, config-3 heads at N={N}, {threads} threads")
+    secs, done = 0.0, 0
+    for (b, h) in heads[:8]:
+        xs = [x[b, h] for x in host]
+        c0 = time.perf_counter()
+        oracle.naive_rows_f32(xs[0], xs[1], xs[2], xs[3], scale, causal, rows_all,
+                              nthreads=threads)
+        secs += time.perf_counter() - c0
+        done += 1
+        if secs >= target_s:
+            break
+    t_est = secs * (B * H) / done
+    cpu = {"value": round(f_total / t_est / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+           "host_cpus": host_cpus(), "kind": "port", "seconds": round(secs, 2),
+           "est_seconds_full_workload": round(t_est, 1),
+           "sample": f"config 3 itself (bf16 causal B={B} H={H} N={N} D={D}, the timed GPU "
+                     f"inputs as float32): {done} of its {B * H} heads, all {N} query rows, "
+                     f"forward + backward in the naive fp32 loops of the reference's CPU "
+                     f"attention (test_forward.cu:21-118, test_backward.cu:21-127), query rows "
+                     f"split over {threads} threads; time scaled by {B * H}/{done}; same FLOP "
+                     f"model as the GPU line"}
+    rows1 = np.arange(8, N, 16, dtype=np.int64)
+    xs = [x[0, 0] for x in host]
+    c0 = time.perf_counter()
+    oracle.naive_rows_f32(xs[0], xs[1], xs[2], xs[3], scale, causal, rows1, nthreads=1)
+    s1 = time.perf_counter() - c0
+    t1_est = s1 * (N / rows1.size) * B * H
+    cpu["single_thread"] = {
+        "value": round(f_total / t1_est / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+        "seconds": round(s1, 2), "est_seconds_full_workload": round(t1_est, 1),
+        "sample": f"every 16th query row ({rows1.size} rows) of head (0, 0) of config 3, one "
+                  f"thread, the same loops; time scaled by {N}/{rows1.size} and by {B * H} heads"}
+    if with_decode:
+        Bd, Hd, LKV, Dd = CFG4["B"], CFG4["H"], CFG4["LKV"], CFG4["D"]
+        nrow = 16
+        log(f"CPU baseline: naive fp32 decode, {nrow} of {Bd * Hd} rows at {LKV} keys")
+        rng = np.random.default_rng(4)
+        qd = rng.standard_normal((nrow, Dd), dtype=np.float32)
+        kd = rng.standard_normal((nrow, LKV, Dd), dtype=np.float32)
+        vd = rng.standard_normal((nrow, LKV, Dd), dtype=np.float32)
+        times = []
+        for _ in range(5):
+            c0 = time.perf_counter()
+            oracle.naive_decode_f32(qd, kd, vd, Dd ** -0.5, nthreads=threads)
+            times.append(time.perf_counter() - c0)
+        td = sorted(times)[2]
+        nbytes = decode_bytes(Bd, Hd, LKV, Dd) * nrow / (Bd * Hd)
+        cpu["decode"] = {
+            "value": round(nbytes / td / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "seconds": round(td, 4),
+            "sample": f"{nrow} of config 4's {Bd * Hd} (batch, head) rows, 1 query against "
+                      f"{LKV} keys, D={Dd}, naive fp32 loops (the reference's naive forward at "
+                      f"a query length of 1), rows over {threads} threads, median of 5 calls; "
+                      f"bytes = config 4's algorithmic fp16 bytes of those rows"}
+        del kd, vd
+    return cpu
 
 
 def main():
@@ -643,7 +733,38 @@ def main():
     ms_per_step = float(np.median(region_ms))
     ms_per_step_mean = ev[0].elapsed_time(ev[-1]) / args.steps
 
-    # Per-kernel durations over a second timed region with the event hook on.
+    # Per-kernel durations. The forward is one kernel per call: K forward calls back to back
+    # between two events give its time per launch directly. A backward call is
+    # delta_ld_kernel then bwd_fused_kernel: K backward calls back to back give their sum, and
+    # the dominant kernel's time is that minus the delta kernel's, which comes from a pass with
+    # the per-launch event hook (events around every launch; they add a few microseconds per
+    # launch, which only this 13-us kernel's figure carries).
+    def back_to_back_ms(fn):
+        for _ in range(3):
+            fn()
+        out = []
+        for _ in range(3):
+            ev[0].record(stream)
+            for _ in range(args.steps):
+                fn()
+            ev[1].record(stream)
+            torch.cuda.synchronize()
+            out.append(ev[0].elapsed_time(ev[1]) / args.steps)
+        return sorted(out)[1]
+
+    def fwd_only():
+        if fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H, N, D,
+               scale, causal, sp) != 0:
+            raise RuntimeError("forward failed")
+
+    def bwd_only():
+        if bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+               do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, N, D, scale,
+               causal, sp) != 0:
+            raise RuntimeError("backward failed")
+
+    fwd_region = back_to_back_ms(fwd_only)
+    bwd_region = back_to_back_ms(bwd_only)
     lib.profile_enable(True)
     for _ in range(args.steps):
         step()
@@ -662,8 +783,20 @@ def main():
     alg = {"forward": f_fwd, "backward_dq_dkdv": f_bwd, "backward_dq": f_bwd / 5,
            "backward_dkdv": f_bwd * 4 / 5}
     suffix = f"_bf16_d{D}"
-    k_ms = {label[:-len(suffix)]: tot / n for label, (n, tot) in kernels.items()
-            if label.endswith(suffix) and n}
+    k_ms_hook = {label[:-len(suffix)]: tot / n for label, (n, tot) in kernels.items()
+                 if label.endswith(suffix) and n}
+    # Per-launch times from the back-to-back regions (the hook's figure beside each).
+    k_ms = dict(k_ms_hook)
+    method = {}
+    if "forward" in k_ms:
+        k_ms["forward"] = fwd_region
+        method["forward"] = "back-to-back forward calls between two events"
+    others = sum(v2 for k2, v2 in k_ms_hook.items()
+                 if k2.startswith("backward") and k2 != "backward_dq_dkdv")
+    if "backward_dq_dkdv" in k_ms:
+        k_ms["backward_dq_dkdv"] = bwd_region - others
+        method["backward_dq_dkdv"] = ("back-to-back backward calls between two events, minus "
+                                      "the delta kernel's per-launch hook time")
     rooflines = []
     for name, flop in alg.items():
         if name not in k_ms:
@@ -673,12 +806,19 @@ def main():
         rooflines.append({"kernel": name + suffix, "bound": "mfma", "achieved": round(ach, 2),
                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                           "frac": round(ach / PEAK_BF16_TFLOPS, 4), "avg_ms": round(ms, 4),
+                          "avg_ms_event_pairs": round(k_ms_hook[name], 4),
+                          "timing": method.get(name, "per-launch event hook"),
                           "alg_flop_per_launch": flop})
     dominant = max(rooflines, key=lambda r: r["avg_ms"])
     roofline = {k2: dominant[k2] for k2 in ("bound", "achieved", "peak", "unit", "frac")}
     roofline["traffic"] = committed_traffic(dominant["kernel"])
+    roofline["traffic_source"] = (
+        "not measured in this run: the rocprofv3 FETCH_SIZE / WRITE_SIZE figure committed in "
+        "profiles/hbm_traffic_pmc.md for this kernel (bytes per launch; its range over runs is "
+        "listed there)")
     roofline["kernel"] = dominant["kernel"]
     roofline["avg_ms"] = dominant["avg_ms"]
+    roofline["timing"] = dominant["timing"]
 
     # ---------------- bounded parity check on the timed data ----------------
     parity = None
@@ -872,37 +1012,8 @@ def main():
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
     if not args.no_cpu_baseline:
-        import oracle
-
-        threads = host_threads()
-        heads = args.cpu_heads or threads
-        ncpu = args.cpu_seq
-        log(f"CPU baseline: naive fp32 fwd+bwd on {heads} heads of N={ncpu}, {threads} threads")
-        sample = (1, heads, ncpu, D)
-        xs = [synth.normal(s, sample) for s in (1, 2, 3, 4)]
-        c0 = time.perf_counter()
-        oracle.naive_forward_f32(xs[0], xs[1], xs[2], scale, causal, nthreads=threads)
-        oracle.naive_backward_f32(xs[0], xs[1], xs[2], xs[3], scale, causal, nthreads=threads)
-        secs = time.perf_counter() - c0
-        f_sample = flops_fwd(1, heads, ncpu, D, causal) * 3.5
-        cpu = {"value": round(f_sample / secs / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-               "kind": "port", "seconds": round(secs, 2),
-               "sample": f"config-3 head shape with N={ncpu} (config 3: {N}; the naive loops "
-                         f"parallelize over heads only, so N bounds the time), B=1 H={heads}, "
-                         f"fwd+bwd, naive O(N^2) fp32 (reference test_forward.cu:21-118 / "
-                         f"test_backward.cu:21-127 restated in C), one thread per head, same "
-                         f"FLOP model"}
-        # One thread on one head of half the length (a quarter of a head's work at N = ncpu).
-        n1 = max(64, ncpu // 2)
-        x1 = [x[:, :1, :n1] for x in xs]
-        c0 = time.perf_counter()
-        oracle.naive_forward_f32(x1[0], x1[1], x1[2], scale, causal, nthreads=1)
-        oracle.naive_backward_f32(x1[0], x1[1], x1[2], x1[3], scale, causal, nthreads=1)
-        secs1 = time.perf_counter() - c0
-        cpu["single_thread"] = {
-            "value": round(flops_fwd(1, 1, n1, D, causal) * 3.5 / secs1 / 1e12, 6),
-            "unit": "TFLOP/s", "cores": 1, "seconds": round(secs1, 2),
-            "sample": f"the same loops on one head of N={n1}, one thread"}
+        cpu = cpu_baseline(host, B, H, N, D, scale, causal, args.cpu_seconds,
+                           with_decode=not args.no_decode)
 
     out = {
         "metric": "fwd+bwd TFLOP/s (bf16 causal N=4096 D=128) + decode HBM GB/s at 32k KV",
@@ -940,7 +1051,10 @@ def main():
         "cpu_baseline": cpu,
     }
     if cpu:
+        # Same problem on both sides: config 3's fwd + bwd (and config 4's decode bytes).
         out["cpu_baseline"]["gpu_speedup"] = round(value / cpu["value"], 1)
+        if decode and "decode" in cpu:
+            cpu["decode"]["gpu_speedup"] = round(decode["value"] / cpu["decode"]["value"], 1)
     print(json.dumps(out), flush=True)
     return 0
 
