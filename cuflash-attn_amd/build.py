@@ -109,6 +109,61 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     return LIB_PATH
 
 
+SANITIZE_DIR = os.path.join(BUILD_DIR, "sanitize")
+SANITIZE_LIB = os.path.join(SANITIZE_DIR, LIB_NAME)
+# AddressSanitizer + UndefinedBehaviorSanitizer on the host code only (the reference's
+# ENABLE_ASAN / ENABLE_UBSAN options, CMakeLists.txt:32-33, 100-114): each -fsanitize= goes to
+# the host compilation through -Xarch_host, so the gfx950 code objects are built exactly as in
+# the release library. The library links the shared sanitizer runtime; a process that loads it
+# must preload that runtime (sanitizer_runtime()).
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=undefined",
+                  "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-g"]
+
+
+def sanitizer_runtime() -> str:
+    """ROCm's clang AddressSanitizer runtime (it carries the UBSan handlers as well)."""
+    out = subprocess.run([hipcc(), "--print-file-name=libclang_rt.asan-x86_64.so"],
+                         capture_output=True, text=True).stdout.strip()
+    if not out or not os.path.exists(out):
+        import glob
+
+        hits = glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so")
+        if not hits:
+            raise RuntimeError("clang AddressSanitizer runtime not found")
+        out = hits[0]
+    return out
+
+
+def build_sanitized(jobs: int = 4, verbose: bool = True) -> str:
+    """The library with the host code under ASan + UBSan, in build/sanitize/. Returns its path."""
+    obj_dir = os.path.join(SANITIZE_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    objs = [os.path.join(obj_dir, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
+
+    def comp(src, obj):
+        cmd = [hipcc(), "-x", "hip", *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *SANITIZE_FLAGS,
+               "-c", os.path.join(CSRC, src), "-o", obj]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{proc.stdout}\n{proc.stderr}")
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
+        for f in [pool.submit(comp, s, o) for s, o in zip(SOURCES, objs)]:
+            f.result()
+    tmp = SANITIZE_LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host",
+           "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-Xarch_host",
+           "-shared-libasan", *objs, "-o", tmp]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, SANITIZE_LIB)
+    if verbose:
+        print(f"built {SANITIZE_LIB}")
+    return SANITIZE_LIB
+
+
 def _link_release() -> None:
     """Points build/release/libcuflash_attn.so at ../libcuflash_attn.so (relative, so the link
     stays valid when the tree is copied elsewhere)."""
@@ -176,8 +231,13 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("--install", metavar="PREFIX", default=None)
+    ap.add_argument("--sanitize", action="store_true",
+                    help="build build/sanitize/libcuflash_attn.so, host code under ASan + UBSan")
     args = ap.parse_args()
     try:
+        if args.sanitize:
+            build_sanitized(args.jobs)
+            sys.exit(0)
         build(args.jobs)
         if args.install:
             install(args.install)

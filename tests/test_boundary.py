@@ -21,6 +21,13 @@ from conftest import REPO
 
 HEADER = os.path.join(REPO, "include", "cuflash", "flash_attention.h")
 
+# The default search order is only what decides the library when $CUFLASH_LIB (the reference
+# caller's override, test_pytorch_comparison.py:158-180) does not name one, as in the run of
+# this suite against the sanitizer build (tests/test_host_sanitizers.py).
+default_search_only = pytest.mark.skipif(
+    bool(os.environ.get("CUFLASH_LIB")),
+    reason="$CUFLASH_LIB names the library; the default search order is checked without it")
+
 
 def _declared_c_symbols():
     text = open(HEADER).read()
@@ -28,6 +35,7 @@ def _declared_c_symbols():
     return sorted(set(re.findall(r"CUFLASH_EXPORT\s+[\w\s\*]+?\b(cuflash_\w+)\s*\(", c_part)))
 
 
+@default_search_only
 def test_library_loads_from_reference_search_path(lib):
     assert lib.path.endswith(os.path.join("build", "libcuflash_attn.so"))
     assert lib.version() == "0.6.0"
@@ -35,7 +43,7 @@ def test_library_loads_from_reference_search_path(lib):
 
 def test_every_declared_symbol_is_exported(lib):
     declared = _declared_c_symbols()
-    assert len(declared) == 26, declared
+    assert len(declared) == 27, declared
     out = subprocess.run(["nm", "-D", "--defined-only", lib.path], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
@@ -308,6 +316,7 @@ EXAMPLE_SEARCH = ("build/release/libcuflash_attn.so", "build/debug/libcuflash_at
                   "/usr/local/lib/libcuflash_attn.so", "/usr/lib/libcuflash_attn.so")
 
 
+@default_search_only
 def test_example_caller_search_path_finds_the_library(lib):
     found = None
     for p in EXAMPLE_SEARCH:
@@ -325,6 +334,7 @@ def test_example_caller_search_path_finds_the_library(lib):
     assert handle.cuflash_error_string(0) == b"Success"
 
 
+@default_search_only
 def test_test_caller_search_path_finds_the_library(lib):
     # tests/integration/test_pytorch_comparison.py:158-180 without $CUFLASH_LIB: build/ first.
     presets = ("default", "release", "release-fast-math", "minimal", "Release", "Debug")
