@@ -106,10 +106,22 @@ hipMemPool_t workspace_pool();
 // process ends. hipStreamPerThread names a different stream in every host thread, so it is not
 // cached (stream_cached_buffer returns false), nor is a stream that is being captured into a
 // graph: every replay of the graph would use the buffer, after later calls had replaced it.
+// The buffers of all streams of one device total at most kStreamCacheTotalBytes: a call whose
+// stream would need a new or larger cached buffer beyond that gets a per-call workspace instead
+// (stream_cached_buffer returns false), so an application that creates a stream per request does
+// not grow device memory without bound. Nothing is evicted (a cached stream handle may already
+// be destroyed, so its buffer cannot be freed stream-ordered); cuflash_release_workspaces()
+// frees them all.
 constexpr size_t kStreamCacheBytes = size_t(64) << 20;
+constexpr size_t kStreamCacheTotalBytes = size_t(256) << 20;
 struct StreamCacheEntry;
 bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
                           std::unique_lock<std::mutex>* lock, FlashAttentionError* err);
+
+// cuflash_release_workspaces: waits for the current device, then frees every cached buffer of
+// its streams. CUDA_ERROR if the device wait fails or a buffer is in use by a call on another
+// host thread (that buffer is kept).
+FlashAttentionError release_stream_buffers();
 
 // Whether `stream` is being captured into a graph (false if that cannot be determined).
 bool stream_capturing(hipStream_t stream);

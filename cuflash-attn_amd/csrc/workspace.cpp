@@ -67,6 +67,7 @@ struct StreamCacheEntry {
 namespace {
 std::mutex g_cache_mutex;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamCacheEntry>> g_cache;
+size_t g_cache_bytes[kMaxDevices] = {};  // bytes of the cached buffers per device
 }  // namespace
 
 bool stream_capturing(hipStream_t stream) {
@@ -82,28 +83,44 @@ bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
                           std::unique_lock<std::mutex>* lock, FlashAttentionError* err) {
     if (stream == hipStreamPerThread || stream_capturing(stream)) return false;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         (void)hipGetLastError();
         return false;
     }
     StreamCacheEntry* e = nullptr;
     {
         std::lock_guard<std::mutex> guard(g_cache_mutex);
-        std::unique_ptr<StreamCacheEntry>& slot = g_cache[{dev, stream}];
-        if (!slot) slot.reset(new StreamCacheEntry());
-        e = slot.get();
+        auto it = g_cache.find({dev, stream});
+        if (it == g_cache.end()) {
+            if (g_cache_bytes[dev] >= kStreamCacheTotalBytes) return false;  // no new entries
+            it = g_cache.emplace(std::make_pair(dev, stream),
+                                 std::unique_ptr<StreamCacheEntry>(new StreamCacheEntry()))
+                     .first;
+        }
+        e = it->second.get();
     }
     std::unique_lock<std::mutex> use(e->use);
     if (e->bytes < bytes) {
         // Grow to at least twice the old size (in whole MiB, at most kStreamCacheBytes).
         size_t want = std::max(bytes, std::min(2 * e->bytes, kStreamCacheBytes));
         want = std::min(kStreamCacheBytes, (want + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1));
+        {
+            // The device's cached total stays within kStreamCacheTotalBytes: past it this call
+            // takes a per-call workspace and the stream keeps its current buffer.
+            std::lock_guard<std::mutex> guard(g_cache_mutex);
+            if (g_cache_bytes[dev] - e->bytes + want > kStreamCacheTotalBytes) return false;
+            g_cache_bytes[dev] += want - e->bytes;
+        }
         void* p = nullptr;
         hipMemPool_t pool = workspace_pool();
         const hipError_t r = pool ? hipMallocFromPoolAsync(&p, want, pool, stream)
                                   : hipMallocAsync(&p, want, stream);
         if (r != hipSuccess) {
             (void)hipGetLastError();
+            {
+                std::lock_guard<std::mutex> guard(g_cache_mutex);
+                g_cache_bytes[dev] -= want - e->bytes;
+            }
             *err = r == hipErrorOutOfMemory ? FlashAttentionError::OUT_OF_MEMORY
                                             : FlashAttentionError::CUDA_ERROR;
             *out = nullptr;
@@ -117,6 +134,44 @@ bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
     *err = FlashAttentionError::SUCCESS;
     *lock = std::move(use);
     return true;
+}
+
+FlashAttentionError release_stream_buffers() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return FlashAttentionError::CUDA_ERROR;
+    }
+    // Every stream's earlier work has finished before a buffer goes (whether or not its stream
+    // still exists), then the buffers go back to the pool.
+    if (hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return FlashAttentionError::CUDA_ERROR;
+    }
+    std::lock_guard<std::mutex> guard(g_cache_mutex);
+    FlashAttentionError status = FlashAttentionError::SUCCESS;
+    for (auto it = g_cache.begin(); it != g_cache.end();) {
+        if (it->first.first != dev) {
+            ++it;
+            continue;
+        }
+        StreamCacheEntry* e = it->second.get();
+        std::unique_lock<std::mutex> use(e->use, std::try_to_lock);
+        if (!use.owns_lock()) {  // a call on another host thread is enqueuing with it
+            status = FlashAttentionError::CUDA_ERROR;
+            ++it;
+            continue;
+        }
+        // Stream-ordered free on the null stream: nothing is pending on any stream any more.
+        if (e->ptr && hipFreeAsync(e->ptr, nullptr) != hipSuccess) {
+            (void)hipGetLastError();
+            status = FlashAttentionError::CUDA_ERROR;
+        }
+        g_cache_bytes[dev] -= e->bytes;
+        use.unlock();
+        it = g_cache.erase(it);
+    }
+    return status;
 }
 
 int compute_units() {
@@ -141,3 +196,11 @@ int compute_units() {
 
 }  // namespace detail
 }  // namespace cuflash
+
+extern "C" {
+
+int cuflash_release_workspaces(void) {
+    return static_cast<int>(cuflash::detail::release_stream_buffers());
+}
+
+}  // extern "C"

@@ -82,6 +82,7 @@ EXPORTED_SYMBOLS = (
     "cuflash_attention_backward_ext_f32", "cuflash_attention_backward_ext_f16",
     "cuflash_attention_backward_ext_bf16", "cuflash_error_string", "cuflash_version",
     "cuflash_profile_enable", "cuflash_profile_report", "cuflash_attention_decode_noalloc_f16",
+    "cuflash_release_workspaces",
 )
 
 
@@ -116,6 +117,8 @@ class CuFlashLibrary:
         library.cuflash_profile_enable.restype = None
         library.cuflash_profile_report.argtypes = [ctypes.c_char_p, ctypes.c_int]
         library.cuflash_profile_report.restype = ctypes.c_int
+        library.cuflash_release_workspaces.argtypes = []
+        library.cuflash_release_workspaces.restype = ctypes.c_int
 
     def error_string(self, code: int) -> str:
         return self.library.cuflash_error_string(int(code)).decode()

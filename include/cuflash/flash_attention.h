@@ -342,6 +342,17 @@ CUFLASH_EXPORT const char* cuflash_version(void);
 CUFLASH_EXPORT void cuflash_profile_enable(int enabled);
 CUFLASH_EXPORT int cuflash_profile_report(char* buf, int buflen);
 
+// Releases the small per-stream workspaces the library caches on the current device (no
+// reference counterpart; the reference allocates and frees per call). Calls on a stream reuse
+// one device buffer of up to 64 MiB, kept from call to call; the buffers of all streams of a
+// device total at most 256 MiB, past which further streams get per-call workspaces. This call
+// synchronizes the device and frees them all; later calls allocate afresh. Call it before
+// destroying streams that the library has used if new streams may get the same handle values
+// while earlier work could still be in flight, and when the memory is wanted back. Returns 0,
+// or 4 (CUDA_ERROR) if the device wait fails or a buffer is in use by a concurrent call on
+// another host thread (that buffer is kept).
+CUFLASH_EXPORT int cuflash_release_workspaces(void);
+
 #ifdef __cplusplus
 }
 #endif

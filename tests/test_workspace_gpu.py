@@ -155,3 +155,36 @@ def test_concurrent_host_threads_on_one_stream(torch_gpu):
     for r, g in zip(ref, outs):
         for a, b in zip(r, g):
             assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_many_streams_past_the_cache_bound_and_release(torch_gpu):
+    """Ten streams whose decode partials need a 34 MB workspace each: the cached buffers stop at
+    256 MiB per device, so the later streams run with per-call workspaces. Every stream's result
+    equals the serial call's; cuflash_release_workspaces() then returns 0 and calls made
+    afterwards (which cache afresh) give the same results again."""
+    torch = torch_gpu
+    lib = cuflash_attn.load_library()
+    H, kv_len, D, splits = 1024, 1024, 128, 64  # partials 1024 * 64 * 130 * 4 B = 34 MB
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    q = torch.randn((1, H, 1, D), generator=g, device="cuda").half()
+    k = torch.randn((1, H, kv_len, D), generator=g, device="cuda").half()
+    v = torch.randn((1, H, kv_len, D), generator=g, device="cuda").half()
+    o_ref, l_ref = cuflash_attn.flash_attention_decode(q, k, v, num_splits=splits)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(10)]
+    outs = []
+    for s in streams:
+        with torch.cuda.stream(s):
+            outs.append(cuflash_attn.flash_attention_decode(q, k, v, num_splits=splits))
+    torch.cuda.synchronize()
+    for o, lse in outs:
+        assert torch.equal(o, o_ref) and torch.equal(lse, l_ref)
+    assert lib.library.cuflash_release_workspaces() == 0
+    for s in streams[:3]:
+        with torch.cuda.stream(s):
+            o, lse = cuflash_attn.flash_attention_decode(q, k, v, num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(lse, l_ref)
+    assert lib.library.cuflash_release_workspaces() == 0
