@@ -77,10 +77,18 @@ def test_config2_fp16_noncausal(torch_gpu):
         assert max_abs(l_np[sl], l_ref) <= TOL16
 
 
-def _fwd_bwd_config(torch_gpu, B, H, N, D, std, fwd_heads, dq_heads, dkdv_heads, row_step):
-    """Forward + backward at full size. O and L are compared on `fwd_heads`; dQ on every row of
-    `dq_heads` and dK, dV on every row of `dkdv_heads` when row_step is None, else on every
-    row_step-th row plus the edge rows; every head through check_invariants."""
+def _rows(N, step):
+    """Every row (step None), else every step-th row plus the edge rows."""
+    if step is None:
+        return np.arange(N)
+    return np.unique(np.concatenate([np.arange(0, N, step), [1, 2, N - 2, N - 1]]))
+
+
+def _fwd_bwd_config(torch_gpu, B, H, N, D, std, fwd_heads, dq_heads, dkdv_heads, q_row_step,
+                    k_row_step):
+    """Forward + backward at full size. O and L are compared on `fwd_heads`; dQ on the rows
+    _rows(N, q_row_step) of `dq_heads` and dK, dV on the rows _rows(N, k_row_step) of
+    `dkdv_heads`; every head through check_invariants."""
     scale = D ** -0.5
     host, (q, k, v, do) = gpu_inputs((B, H, N, D), "bfloat16", "normal", (1, 2, 3, 4), std)
     o, lse = cuflash_attn.flash_attention_forward(q, k, v, scale=scale, causal=True)
@@ -92,10 +100,7 @@ def _fwd_bwd_config(torch_gpu, B, H, N, D, std, fwd_heads, dq_heads, dkdv_heads,
         assert np.isfinite(t).all()
     check_invariants(host[0], host[1], host[2], got[0], got[1], host[3], got[2], got[3], got[4],
                      scale, n_tol=2e-2)
-    if row_step is None:
-        rows = np.arange(N)
-    else:
-        rows = np.unique(np.concatenate([np.arange(0, N, row_step), [1, 2, N - 2, N - 1]]))
+    q_rows, k_rows = _rows(N, q_row_step), _rows(N, k_row_step)
     none = np.zeros(0, dtype=np.int64)
     for b, h in sorted(set(fwd_heads) | set(dq_heads) | set(dkdv_heads)):
         sl = (slice(b, b + 1), slice(h, h + 1))
@@ -104,8 +109,8 @@ def _fwd_bwd_config(torch_gpu, B, H, N, D, std, fwd_heads, dq_heads, dkdv_heads,
             o_ref, l_ref = oracle.forward(qh, kh, vh, scale, True)
             assert max_abs(got[0][sl], o_ref) <= TOL16, f"O {(b, h)}"
             assert max_abs(got[1][sl], l_ref) <= TOL16, f"L {(b, h)}"
-        qr = rows if (b, h) in dq_heads else none
-        kr = rows if (b, h) in dkdv_heads else none
+        qr = q_rows if (b, h) in dq_heads else none
+        kr = k_rows if (b, h) in dkdv_heads else none
         rq, rk, rv = oracle.backward_rows(qh, kh, vh, doh, scale, True, qr, kr)
         if len(qr):
             assert max_abs(got[2][sl][:, :, qr], rq) <= TOL16, f"dQ {(b, h)}"
@@ -119,14 +124,17 @@ def test_config3_bf16_causal_fwd_bwd(torch_gpu):
     # every row: dK and dV of four heads, dQ of two
     heads4 = ((0, 0), (0, 9), (1, 6), (1, 15))
     _fwd_bwd_config(torch_gpu, 2, 16, 4096, 128, 1.0, fwd_heads=heads4,
-                    dq_heads=((0, 0), (1, 15)), dkdv_heads=heads4, row_step=None)
+                    dq_heads=((0, 0), (1, 15)), dkdv_heads=heads4, q_row_step=None,
+                    k_row_step=None)
 
 
 @pytest.mark.gpu
 def test_config5_bf16_long_context_fwd_bwd(torch_gpu):
+    # dK and dV on every one of the 16384 key rows of two heads (the first and the last), dQ on
+    # every 127th query row of them (the oracle's row-streaming backward: ~10 s per head).
     heads = ((0, 0), (0, 31))
     _fwd_bwd_config(torch_gpu, 1, 32, 16384, 128, 0.5, fwd_heads=heads, dq_heads=heads,
-                    dkdv_heads=heads, row_step=127)
+                    dkdv_heads=heads, q_row_step=127, k_row_step=None)
 
 
 @pytest.mark.gpu
@@ -146,7 +154,11 @@ def test_config4_fp16_decode(torch_gpu, splits):
     torch.cuda.synchronize()
     o_np, l_np = synth.to_numpy(o), synth.to_numpy(lse)
     assert np.isfinite(o_np).all() and np.isfinite(l_np).all()
-    for b, h in ((0, 0), (7, 19), (15, 31)):
+    # 18 (batch, head) rows: one per batch with head (7 b + 3) mod 32 (16 different heads),
+    # plus the first and the last.
+    checked = sorted({(b, (7 * b + 3) % H) for b in range(B)} | {(0, 0), (B - 1, H - 1)})
+    assert len(checked) >= 16
+    for b, h in checked:
         qh = synth.to_numpy(q[b:b + 1, h:h + 1])
         kh = synth.to_numpy(k[b:b + 1, h:h + 1])
         vh = synth.to_numpy(v[b:b + 1, h:h + 1])
