@@ -118,9 +118,11 @@ struct StreamCacheEntry;
 bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
                           std::unique_lock<std::mutex>* lock, FlashAttentionError* err);
 
-// cuflash_release_workspaces: waits for the current device, then frees every cached buffer of
-// its streams. CUDA_ERROR if the device wait fails or a buffer is in use by a call on another
-// host thread (that buffer is kept).
+// cuflash_release_workspaces: takes the cached buffers of the current device's streams away
+// from later calls, waits for the device, then frees them. CUDA_ERROR if the device wait fails
+// (nothing is freed) or a buffer is in use by a call on another host thread (that buffer is
+// kept). A call that looked its stream's buffer up before the release takes a per-call
+// workspace instead.
 FlashAttentionError release_stream_buffers();
 
 // Whether `stream` is being captured into a graph (false if that cannot be determined).

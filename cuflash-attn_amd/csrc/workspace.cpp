@@ -14,6 +14,7 @@
 #include <memory>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "launch.hpp"
 
@@ -62,11 +63,14 @@ struct StreamCacheEntry {
     std::mutex use;  // held by the call that is enqueuing work with the buffer
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool released = false;  // freed by release_stream_buffers (set under `use`)
 };
 
 namespace {
 std::mutex g_cache_mutex;
-std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamCacheEntry>> g_cache;
+// Shared ownership: a call that has looked an entry up keeps it alive while it waits for the
+// entry's lock, also when release_stream_buffers takes the entry out of the map meanwhile.
+std::map<std::pair<int, hipStream_t>, std::shared_ptr<StreamCacheEntry>> g_cache;
 size_t g_cache_bytes[kMaxDevices] = {};  // bytes of the cached buffers per device
 }  // namespace
 
@@ -87,19 +91,22 @@ bool stream_cached_buffer(hipStream_t stream, size_t bytes, void** out,
         (void)hipGetLastError();
         return false;
     }
-    StreamCacheEntry* e = nullptr;
+    std::shared_ptr<StreamCacheEntry> e;
     {
         std::lock_guard<std::mutex> guard(g_cache_mutex);
         auto it = g_cache.find({dev, stream});
         if (it == g_cache.end()) {
-            if (g_cache_bytes[dev] >= kStreamCacheTotalBytes) return false;  // no new entries
-            it = g_cache.emplace(std::make_pair(dev, stream),
-                                 std::unique_ptr<StreamCacheEntry>(new StreamCacheEntry()))
+            // No entry for a stream whose first buffer would not fit under the device total
+            // (an entry that could never hold a buffer would only grow the map).
+            const size_t first = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+            if (g_cache_bytes[dev] + first > kStreamCacheTotalBytes) return false;
+            it = g_cache.emplace(std::make_pair(dev, stream), std::make_shared<StreamCacheEntry>())
                      .first;
         }
-        e = it->second.get();
+        e = it->second;
     }
     std::unique_lock<std::mutex> use(e->use);
+    if (e->released) return false;  // released after the lookup: this call takes a workspace
     if (e->bytes < bytes) {
         // Grow to at least twice the old size (in whole MiB, at most kStreamCacheBytes).
         size_t want = std::max(bytes, std::min(2 * e->bytes, kStreamCacheBytes));
@@ -142,36 +149,48 @@ FlashAttentionError release_stream_buffers() {
         (void)hipGetLastError();
         return FlashAttentionError::CUDA_ERROR;
     }
-    // Every stream's earlier work has finished before a buffer goes (whether or not its stream
-    // still exists), then the buffers go back to the pool.
-    if (hipDeviceSynchronize() != hipSuccess) {
-        (void)hipGetLastError();
-        return FlashAttentionError::CUDA_ERROR;
-    }
+    // The entries are locked first, so that no call can enqueue work with their buffers, then
+    // the device is drained (whether or not the streams still exist), then the buffers go back
+    // to the pool. An entry held by a call on another host thread is kept.
     std::lock_guard<std::mutex> guard(g_cache_mutex);
     FlashAttentionError status = FlashAttentionError::SUCCESS;
-    for (auto it = g_cache.begin(); it != g_cache.end();) {
-        if (it->first.first != dev) {
-            ++it;
-            continue;
-        }
-        StreamCacheEntry* e = it->second.get();
-        std::unique_lock<std::mutex> use(e->use, std::try_to_lock);
-        if (!use.owns_lock()) {  // a call on another host thread is enqueuing with it
+    // `keep` is declared first so that it is destroyed last: the entries outlive their locks.
+    std::vector<std::shared_ptr<StreamCacheEntry>> keep;
+    std::vector<std::unique_lock<std::mutex>> held;
+    for (auto& kv : g_cache) {
+        if (kv.first.first != dev) continue;
+        std::unique_lock<std::mutex> use(kv.second->use, std::try_to_lock);
+        if (use.owns_lock()) {
+            keep.push_back(kv.second);
+            held.push_back(std::move(use));
+        } else {
             status = FlashAttentionError::CUDA_ERROR;
+        }
+    }
+    if (held.empty()) return status;
+    if (hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return FlashAttentionError::CUDA_ERROR;  // nothing freed
+    }
+    for (auto it = g_cache.begin(); it != g_cache.end();) {
+        StreamCacheEntry* e = it->second.get();
+        const bool mine = std::find(keep.begin(), keep.end(), it->second) != keep.end();
+        if (!mine) {
             ++it;
             continue;
         }
-        // Stream-ordered free on the null stream: nothing is pending on any stream any more.
+        // Stream-ordered free on the null stream: nothing is pending on the device any more.
         if (e->ptr && hipFreeAsync(e->ptr, nullptr) != hipSuccess) {
             (void)hipGetLastError();
             status = FlashAttentionError::CUDA_ERROR;
         }
         g_cache_bytes[dev] -= e->bytes;
-        use.unlock();
-        it = g_cache.erase(it);
+        e->ptr = nullptr;
+        e->bytes = 0;
+        e->released = true;
+        it = g_cache.erase(it);  // callers that looked it up keep it alive and see `released`
     }
-    return status;
+    return status;  // `held` unlocks the entries
 }
 
 int compute_units() {

@@ -188,3 +188,57 @@ def test_many_streams_past_the_cache_bound_and_release(torch_gpu):
         torch.cuda.synchronize()
         assert torch.equal(o, o_ref) and torch.equal(lse, l_ref)
     assert lib.library.cuflash_release_workspaces() == 0
+
+
+@pytest.mark.gpu
+def test_release_while_other_threads_call(torch_gpu):
+    """cuflash_release_workspaces() from one host thread while four others run decodes on their
+    own streams: every release returns 0 or CUDA_ERROR (a buffer in use by a call is kept), and
+    every decode result equals the serial call's."""
+    import threading
+
+    torch = torch_gpu
+    lib = cuflash_attn.load_library()
+    H, kv_len, D, splits = 64, 2048, 128, 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(78)
+    q = torch.randn((2, H, 1, D), generator=g, device="cuda").half()
+    k = torch.randn((2, H, kv_len, D), generator=g, device="cuda").half()
+    v = torch.randn((2, H, kv_len, D), generator=g, device="cuda").half()
+    o_ref, l_ref = cuflash_attn.flash_attention_decode(q, k, v, num_splits=splits)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    outs = [[(torch.empty_like(o_ref), torch.empty_like(l_ref)) for _ in range(20)]
+            for _ in streams]
+    fn = lib.fn("decode", "f16")
+    errors, codes = [], []
+    done = threading.Event()
+
+    def worker(i):
+        sp = streams[i].cuda_stream
+        for o, lse in outs[i]:
+            st = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), 2, H,
+                    kv_len, D, D ** -0.5, splits, sp)
+            if st != 0:
+                errors.append((i, st))
+
+    def releaser():
+        while not done.is_set():
+            codes.append(lib.library.cuflash_release_workspaces())
+
+    rel = threading.Thread(target=releaser)
+    rel.start()
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(streams))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    done.set()
+    rel.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    assert codes and set(codes) <= {0, 4}, sorted(set(codes))
+    for per_stream in outs:
+        for o, lse in per_stream:
+            assert torch.equal(o, o_ref) and torch.equal(lse, l_ref)
+    assert lib.library.cuflash_release_workspaces() == 0
