@@ -1172,7 +1172,7 @@ FlashAttentionError run_backward_two_pass(const T* Q, const T* K, const T* V, co
     const long long dthreads = rows * LPR;
     const long long dblocks = (dthreads + 255) / 256;
     if (dblocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    int tok = profile_kernel<T, D>("backward_delta");
+    ProfileEvents tok = profile_kernel<T, D>("backward_delta");
     launch_kernel(tok, (dev::delta_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, o, delta, rows);
     err = from_hip(hipGetLastError());
@@ -1253,7 +1253,7 @@ FlashAttentionError run_backward_fused(const T* Q, const T* K, const T* V, const
     const uint16_t* v = reinterpret_cast<const uint16_t*>(V);
     const uint16_t* go = reinterpret_cast<const uint16_t*>(dO);
 
-    int tok = profile_kernel<T, D>("backward_delta");
+    ProfileEvents tok = profile_kernel<T, D>("backward_delta");
     launch_kernel(tok, (dev::delta_ld_kernel<T, D>), dim3(static_cast<unsigned>(dblocks)), dim3(256),
                        0, stream, go, reinterpret_cast<const uint16_t*>(O), L, ld, sh.Nq, Npad,
                        rows_pad, queues);

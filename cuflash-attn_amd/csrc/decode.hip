@@ -941,7 +941,7 @@ FlashAttentionError run_decode(const T* Q, const T* K, const T* V, T* O, float* 
     float* part_acc = static_cast<float*>(base);
     float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(base) + acc_bytes);
 
-    int tok = profile_kernel<T, D>("decode_split");
+    ProfileEvents tok = profile_kernel<T, D>("decode_split");
     if constexpr (MMA) {
         static_assert((D == 32 || D == 64 || D == 128) && !std::is_same<T, float>::value,
                       "MMA decode shape");

@@ -1631,7 +1631,7 @@ FlashAttentionError run_forward16(const T* Q, const T* K, const T* V, T* O, floa
     long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
     const int coff = sh.Nk - sh.Nq;
-    const int tok = profile_kernel<T, D>("forward");
+    const ProfileEvents tok = profile_kernel<T, D>("forward");
     if constexpr (D == 64) {
         // Launches with at least as many 256-row blocks as CUs: eight-wave workgroups of the
         // sequential kernel (two per CU), except causal ones with fewer than 8192 keys, which
@@ -1738,7 +1738,7 @@ FlashAttentionError run_forward32(const float* Q, const float* K, const float* V
     const int nqb = (sh.Nq + Cfg::BM - 1) / Cfg::BM;
     const long long blocks = static_cast<long long>(nqb) * sh.BH;
     if (blocks > 0x7fffffffLL) return FlashAttentionError::INVALID_DIMENSION;
-    const int tok = profile_kernel<float, D>("forward");
+    const ProfileEvents tok = profile_kernel<float, D>("forward");
     if constexpr (D <= 64) {
         // Fewer workgroups of 128 rows than two per CU: split each 32-row block's keys over
         // the four waves of a workgroup instead (fwd32_split_kernel).

@@ -43,8 +43,8 @@ const char* dtype_tag<__hip_bfloat16>() {
 
 bool profiling_on() { return g_enabled.load(std::memory_order_relaxed) != 0; }
 
-int profile_begin(const char* label) {
-    if (!g_enabled.load(std::memory_order_relaxed)) return -1;
+ProfileEvents profile_begin(const char* label) {
+    if (!g_enabled.load(std::memory_order_relaxed)) return ProfileEvents{};
     Record r;
     r.label = label;
     std::lock_guard<std::mutex> lock(g_mu);
@@ -52,21 +52,14 @@ int profile_begin(const char* label) {
         r.ev = g_free.back();
         g_free.pop_back();
     } else {
-        if (hipEventCreate(&r.ev.start) != hipSuccess) return -1;
+        if (hipEventCreate(&r.ev.start) != hipSuccess) return ProfileEvents{};
         if (hipEventCreate(&r.ev.stop) != hipSuccess) {
             (void)hipEventDestroy(r.ev.start);
-            return -1;
+            return ProfileEvents{};
         }
     }
     g_records.push_back(r);
-    return static_cast<int>(g_records.size()) - 1;
-}
-
-ProfileEvents profile_events(int token) {
-    if (token < 0) return ProfileEvents{};
-    std::lock_guard<std::mutex> lock(g_mu);
-    if (token >= static_cast<int>(g_records.size())) return ProfileEvents{};
-    return g_records[token].ev;
+    return r.ev;
 }
 
 // Pre-creates event pairs so that a timed region's launches find them in the pool.

@@ -21,34 +21,32 @@ namespace detail {
 
 bool profiling_on();
 
-// Returns a token for launch_kernel(), or -1 when profiling is off.
-int profile_begin(const char* label);
-
 struct ProfileEvents {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
 };
-// The event pair of a token (both null for -1).
-ProfileEvents profile_events(int token);
+
+// Records a launch under `label` and returns the event pair its launch_kernel() fills; both
+// events are null when profiling is off (or no pair could be created).
+ProfileEvents profile_begin(const char* label);
 
 template <typename T>
 const char* dtype_tag();
 
 // profile_begin with the label "<kernel>_<dtype>_d<head_dim>".
 template <typename T, int D>
-int profile_kernel(const char* kernel) {
-    if (!profiling_on()) return -1;
+ProfileEvents profile_kernel(const char* kernel) {
+    if (!profiling_on()) return ProfileEvents{};
     char label[96];
     std::snprintf(label, sizeof(label), "%s_%s_d%d", kernel, dtype_tag<T>(), D);
     return profile_begin(label);
 }
 
-// Launches `kernel` on `stream`; with a profiling token, its events record the kernel's own
-// start and end.
+// Launches `kernel` on `stream`; with the event pair of a profiled launch, the events record
+// the kernel's own start and end.
 template <typename... Args, typename F>
-void launch_kernel(int token, F kernel, const dim3& grid, const dim3& block, uint32_t lds_bytes,
-                   hipStream_t stream, Args... args) {
-    const ProfileEvents ev = profile_events(token);
+void launch_kernel(const ProfileEvents& ev, F kernel, const dim3& grid, const dim3& block,
+                   uint32_t lds_bytes, hipStream_t stream, Args... args) {
     hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, stream, ev.start, ev.stop, 0u, args...);
 }
 
