@@ -161,6 +161,20 @@ def build_sanitized(jobs: int = 4, verbose: bool = True) -> str:
     os.replace(tmp, SANITIZE_LIB)
     if verbose:
         print(f"built {SANITIZE_LIB}")
+    # The GPU-side exercise of the sanitized host code (tests/cpp/host_sanitizer_driver.cpp),
+    # itself instrumented and linked against the shared sanitizer runtime next to the library.
+    runtime_dir = os.path.dirname(sanitizer_runtime())
+    out = os.path.join(SANITIZE_DIR, "host_sanitizer_driver")
+    cmd = [hipcc(), "-x", "hip", "--offload-arch=gfx950", "-O1", "-std=c++17", *SANITIZE_FLAGS,
+           "-I" + INCLUDE, os.path.join(TEST_SRC, "host_sanitizer_driver.cpp"), "-x", "none",
+           SANITIZE_LIB, "-Xarch_host", "-shared-libasan", "-Wl,-rpath,$ORIGIN",
+           "-Wl,-rpath," + runtime_dir, "-lpthread", "-o", out + ".tmp"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for host_sanitizer_driver.cpp:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print(f"built {out}")
     return SANITIZE_LIB
 
 
