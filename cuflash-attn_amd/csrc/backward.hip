@@ -548,26 +548,10 @@ __global__ void __launch_bounds__(256)
 // budget allows two workgroups per CU at head_dim 64 and 128, so the two waves of each SIMD hide
 // each other's latencies (one at head_dim 256).
 // TileGroups<D> (tile_groups.hpp) gives these layouts per head_dim.
-
-// Work item id -> (head, rank) of a queue of `heads` * `per_head` items. Rank-major
-// (head_rank_order: rank 0, the longest item, of every head first) unless `head_major`: then,
-// with the heads split over the XCDs as in head_rank_order, an XCD takes all ranks of one head
-// before the next head, so the items of a head that run at the same time read the same rows of
-// Q / dO (dkdv) or K / V (dq) and share them in the XCD's L2 and the Infinity Cache. Measured,
-// bitwise equal: dq items head-major 0.3-3% faster at every shape (config 3 447.6 -> 443.3 us,
-// config 5 -2.9%); dkdv items head-major 2.2-3.5% faster at config 5 but up to 11% slower at
-// config 3 causal, where a head's longest items then start too late to finish with the rest.
-__device__ __forceinline__ void item_order(int bid, int heads, int per_head, bool head_major,
-                                           int& h, int& r) {
-    if (head_major && heads % kNumXcd == 0) {
-        const int hpx = heads / kNumXcd;
-        const int k = bid / kNumXcd;
-        h = (bid % kNumXcd) * hpx + k / per_head;
-        r = k % per_head;
-    } else {
-        head_rank_order(bid, heads, h, r);
-    }
-}
+// Item orders (item_order, common.hpp), measured bitwise equal: dq items head-major 0.3-3%
+// faster at every shape (config 3 447.6 -> 443.3 us, config 5 -2.9%); dkdv items head-major
+// 2.2-3.5% faster at config 5 but up to 11% slower at config 3 causal, where a head's longest
+// items then start too late to finish with the rest.
 
 // Key-stationary part of work item `bid` of heads * nkb (kb = 0 has the most work; the order
 // of the ids is item_order's, bit 0 of `order`); smem
@@ -1060,8 +1044,9 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
 // even XCDs take the dkdv items (128 keys each, BHkv * nkb of them), odd XCDs the dq items
 // (128 query rows each, BH * nqb), each XCD the ids congruent to x / 2 modulo 4, in increasing
 // order: every XCD keeps its own heads (their tiles stay in its L2), in the item order `order`
-// selects (bit 0: dkdv items head-major, bit 1: dq items head-major; item_order). A workgroup whose own queue is empty takes from the next XCD's queue, then from the
-// others, and exits when every queue is empty. The dq items need about 70% of the dkdv items'
+// selects (bit 0: dkdv items head-major, bit 1: dq items head-major; item_order). A workgroup
+// whose own queue is empty takes from the next XCD's queue, then from the others, and exits
+// when every queue is empty. The dq items need about 70% of the dkdv items'
 // time, so without the hand-over the dq XCDs would idle for the last third of the launch.
 // Counters are cleared by delta_ld_kernel; every workgroup ends after at most one failed pass
 // over the queues, so the launch always drains.

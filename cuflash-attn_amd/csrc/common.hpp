@@ -391,5 +391,23 @@ __device__ __forceinline__ void head_rank_order(int bid, int BH, int& bh, int& r
     }
 }
 
+// Work item / workgroup id -> (head, rank) for `heads` * `per_head` items whose items of one head
+// share K/V (forward, dq) or Q/dO (dkdv). Rank-major (head_rank_order: rank 0 of every head of an
+// XCD first, the longest item under a causal mask) unless `head_major`: then, with the heads
+// split over the XCDs as in head_rank_order, an XCD takes all ranks of one head before the next
+// head, so the items of a head that run at the same time read the same rows and share them in
+// the XCD's L2 and the Infinity Cache, at the price of starting a head's longest items late.
+__device__ __forceinline__ void item_order(int bid, int heads, int per_head, bool head_major,
+                                           int& h, int& r) {
+    if (head_major && heads % kNumXcd == 0) {
+        const int hpx = heads / kNumXcd;
+        const int k = bid / kNumXcd;
+        h = (bid % kNumXcd) * hpx + k / per_head;
+        r = k % per_head;
+    } else {
+        head_rank_order(bid, heads, h, r);
+    }
+}
+
 }  // namespace dev
 }  // namespace cuflash

@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
 
     int bh, rank;
-    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    item_order(blockIdx.x, gridDim.x / nqb, nqb, causal == 0, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(64 * NW, 1)
     __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
 
     int bh, rank;
-    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    item_order(blockIdx.x, gridDim.x / nqb, nqb, causal == 0, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -722,7 +722,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW)
     __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
 
     int bh, rank;
-    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    item_order(blockIdx.x, gridDim.x / nqb, nqb, causal == 0, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1063,7 +1063,7 @@ __global__ void __launch_bounds__(64 * NW, 16 / NW)
     __shared__ __attribute__((aligned(1024))) unsigned char Vb1[TILE];
 
     int bh, rank;
-    head_rank_order(blockIdx.x, gridDim.x / nqb, bh, rank);
+    item_order(blockIdx.x, gridDim.x / nqb, nqb, causal == 0, bh, rank);
     const int qb = causal ? nqb - 1 - rank : rank;  // causal: longest query blocks first
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
