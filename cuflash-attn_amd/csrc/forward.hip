@@ -19,7 +19,9 @@
 // registers). Each lane therefore owns one query row of O, and the softmax rescale is a per-lane
 // multiply. The next K/V block is loaded (LDS-DMA for fp16 / bf16, through registers for fp32)
 // while the current one is consumed.
-// Causal launches process the longest query blocks first; blocks of one head share an XCD.
+// Blocks of one head share an XCD (item_order); causal launches process the longest query
+// blocks first, non-causal ones the blocks of one head after another (equal blocks: the blocks
+// of a head then run together and share their K/V rows in L2).
 //
 // Shapes: Q and O are [BH, Nq, D], K and V are [BH / group, Nk, D] (query head bh reads
 // key/value head bh / group), L is [BH, Nq]. With a causal mask query i sees the keys
