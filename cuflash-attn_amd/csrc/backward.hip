@@ -509,8 +509,17 @@ __global__ void __launch_bounds__(256, 1)
 // ------------------------------------------------------------------------------------------
 // Row statistics for bwd_fused_kernel: LD[bh * Npad + r] = (L * log2(e), D) for r < N and
 // (+inf, 0) for the padding rows N <= r < Npad (Npad = N rounded up to 32), so that P = 0 there
-// without any masking. N is the query length. Block 0 also clears the kNumXcd work-queue
-// counters of the bwd_fused_kernel launch that follows on the stream.
+// without any masking. At head_dim 64 (neg_d_rows) each 32 rows are stored instead as the 32
+// values L * log2(e), then the 32 values -D (same 256 bytes): the dkdv items then start their
+// dP MFMA chain from -D read straight into the accumulator, so dS = P (dP - D) takes one
+// multiply per score instead of a subtract and a multiply (head_dim 64, where the vector work
+// sets the time: backward 3-5% faster; at 128 the same form measured 1.5% slower non-causal and
+// at 32 mixed, so they keep the interleaved pairs). N is the query length. Block 0 also clears
+// the kNumXcd work-queue counters of the bwd_fused_kernel launch that follows on the stream.
+template <int D>
+constexpr bool neg_d_rows() {
+    return D == 64;
+}
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
     delta_ld_kernel(const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O,
@@ -532,8 +541,16 @@ __global__ void __launch_bounds__(256)
     }
 #pragma unroll
     for (int w = LPR / 2; w > 0; w >>= 1) s += xor_shuffle(s, w);
-    if (prow < rows_pad && part == 0)
-        LD[prow] = real ? make_float2(L[bh * N + r] * kLog2e, s) : make_float2(INFINITY, 0.0f);
+    if (prow < rows_pad && part == 0) {
+        const float lv = real ? L[bh * N + r] * kLog2e : INFINITY;
+        if constexpr (neg_d_rows<D>()) {
+            float* blk = reinterpret_cast<float*>(LD) + (prow >> 5) * 64 + (prow & 31);
+            blk[0] = lv;
+            blk[32] = real ? -s : 0.0f;
+        } else {
+            LD[prow] = make_float2(lv, real ? s : 0.0f);
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -699,12 +716,23 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         const unsigned char* qt = smem + b * SET;
         const unsigned char* ot = qt + QT;
         const float2* ldv = reinterpret_cast<const float2*>(qt + 2 * QT);
+        const float* ldf = reinterpret_cast<const float*>(ldv);  // neg_d_rows: 32 L, then 32 -D
 
         // S = Q K^T and dP = dO V^T: rows = queries, lane = key. Operand i (i even: Q, odd: dO;
         // k-step i / 2) is read kAhead MFMAs before its product; the scheduling fences keep the
         // compiler from undoing that order.
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
+        if constexpr (neg_d_rows<D>()) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const f32x4 nd = *reinterpret_cast<const f32x4*>(&ldf[32 + 8 * a + 4 * g2]);
+                dp[4 * a + 0] = nd[0];
+                dp[4 * a + 1] = nd[1];
+                dp[4 * a + 2] = nd[2];
+                dp[4 * a + 3] = nd[3];
+            }
+        }
         {
             constexpr int kAhead = 3;
             constexpr int kMma = 2 * (D / 16);
@@ -742,16 +770,27 @@ __device__ __forceinline__ void dkdv_lds_tiles(const uint16_t* __restrict__ Q,
         frag bp[2], bs[2];
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2]);
-            const f32x4 y = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2 + 2]);
-            const float lv[4] = {x[0], x[2], y[0], y[2]};
-            const float dd[4] = {x[1], x[3], y[1], y[3]};
+            if constexpr (neg_d_rows<D>()) {
+                const f32x4 lv = *reinterpret_cast<const f32x4*>(&ldf[8 * a + 4 * g2]);
 #pragma unroll
-            for (int k2 = 0; k2 < 4; ++k2) {
-                const int r = 4 * a + k2;
-                const float p = fast_exp2(fmaf(s[r], cs, -lv[k2]));
-                s[r] = p;
-                dp[r] = p * (dp[r] - dd[k2]);
+                for (int k2 = 0; k2 < 4; ++k2) {
+                    const int r = 4 * a + k2;
+                    const float p = fast_exp2(fmaf(s[r], cs, -lv[k2]));
+                    s[r] = p;
+                    dp[r] = p * dp[r];  // the dP chain started from -D
+                }
+            } else {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2]);
+                const f32x4 y = *reinterpret_cast<const f32x4*>(&ldv[8 * a + 4 * g2 + 2]);
+                const float lv[4] = {x[0], x[2], y[0], y[2]};
+                const float dd[4] = {x[1], x[3], y[1], y[3]};
+#pragma unroll
+                for (int k2 = 0; k2 < 4; ++k2) {
+                    const int r = 4 * a + k2;
+                    const float p = fast_exp2(fmaf(s[r], cs, -lv[k2]));
+                    s[r] = p;
+                    dp[r] = p * (dp[r] - dd[k2]);
+                }
             }
         }
 #pragma unroll
@@ -896,8 +935,18 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
         qf[ks] = as_frag<T>(qv);
         of[ks] = as_frag<T>(ov);
     }
-    // (L log2 e, D) of this lane's query; padding rows give P = 0.
-    const float2 ldq = (q < Npad) ? LD[static_cast<size_t>(bh) * Npad + q] : make_float2(INFINITY, 0.0f);
+    // (L log2 e, D) of this lane's query (stored as -D in the neg_d_rows layout); padding rows
+    // give P = 0.
+    float2 ldq = make_float2(INFINITY, 0.0f);
+    if (q < Npad) {
+        if constexpr (neg_d_rows<D>()) {
+            const float* blk = reinterpret_cast<const float*>(LD) +
+                               (static_cast<size_t>(bh) * Npad + (q & ~31)) * 2 + (q & 31);
+            ldq = make_float2(blk[0], -blk[32]);
+        } else {
+            ldq = LD[static_cast<size_t>(bh) * Npad + q];
+        }
+    }
 
     const int ld_row = G::ld_row(lane);
     const int ld_col = G::ld_col(lane);
