@@ -1003,6 +1003,10 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
         // V; k-step i / 2) is read kAhead MFMAs before its product.
         f32x16 s = f32x16{};
         f32x16 dp = f32x16{};
+        if constexpr (neg_d_rows<D>()) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] = -ldq.y;
+        }
         {
             constexpr int kAhead = 3;
             constexpr int kMma = 2 * (D / 16);
@@ -1035,7 +1039,10 @@ __device__ __forceinline__ void dq_lds_tiles(const uint16_t* __restrict__ Q,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const float p = fast_exp2(fmaf(s[r], cs, -ldq.x));
-            s[r] = p * (dp[r] - ldq.y);  // dS^T
+            if constexpr (neg_d_rows<D>())
+                s[r] = p * dp[r];  // dS^T (the dP chain started from -D)
+            else
+                s[r] = p * (dp[r] - ldq.y);  // dS^T
         }
         // dQ^T += K^T dS^T (k = the block's 32 keys; K^T by transpose reads). Operand i
         // (j = i / 4, dt = i % 4) is read kAhead MFMAs ahead.
